@@ -1,0 +1,81 @@
+// Shared host/device layout of the attention plan's device metadata.
+//
+// The reference hands attention a FlashInfer plan (src/flashinfer_attention.cu:14-34)
+// or, in the ATen build, per-sequence gather indices and masks
+// (src/portable_gpu_ops.cpp:27-38).  Here the host planner turns the same
+// CSR metadata (qo / kv / pages / last) into flat work lists that the HIP
+// kernels walk with a grid fixed by the plan capacity.
+#pragma once
+#include <stdint.h>
+
+namespace feattn {
+
+constexpr int kHeadDim = 128;  // the only head size the reference builds (flashinfer_attention.cu:23)
+constexpr int kTileTokens = 64;  // tokens per KV tile of the MFMA tile kernel (4 pages of 16)
+constexpr int kTileCols = 128;   // (q row, head) columns per tile work item (4 waves x 32)
+constexpr int kDecodeCols = 16;  // max (q row, head) columns of one decode work item (one MFMA N block)
+
+// Per sequence, derived from the CSR metadata exactly as the reference ATen
+// plan does (portable_gpu_ops.cpp:30): len = (kv[b+1]-kv[b]-1)*page + last[b].
+struct SeqInfo {
+  int32_t qo;        // first query row of the sequence (qo[b])
+  int32_t qlen;      // query rows (qo[b+1]-qo[b])
+  int32_t len;       // tokens in the KV cache for this sequence, current chunk included
+  int32_t page_off;  // index of the sequence's first page id in the page table (kv[b])
+};
+
+// One unit of kernel work: query rows [q0, q0+nq) of sequence `seq` (all the
+// query heads of kv head `kvh`) against tokens [t0, t1).  part < 0 writes
+// the normalised result to `out`; part >= 0 writes it, with its log2
+// log-sum-exp, to partial slot part + (row - q0) for the merge kernel.
+struct WorkItem {
+  int32_t seq;
+  int32_t q0;
+  int32_t nq;
+  int32_t kvh;
+  int32_t t0;
+  int32_t t1;
+  int32_t part;
+  int32_t cost;  // planner's cost estimate; unused on the device
+};
+
+// One query row whose tokens were split over `nsplit` work items.  Split s
+// of this row lives in partial slot part + s*stride.
+struct MergeRow {
+  int32_t row;
+  int32_t part;
+  int32_t nsplit;
+  int32_t stride;
+};
+
+// Kernel arguments shared by the decode and tile kernels.
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  uint16_t* out;
+  float* lse;             // [rows][hq] natural log, may be null
+  const SeqInfo* seqs;
+  const int32_t* pages;
+  const WorkItem* items;
+  const int32_t* n_items;  // device-resident count (graph replays read the current one)
+  float* part_o;           // [slots][hq][128] fp32, normalised per split
+  float* part_lse;         // [slots][hq] log2 domain
+  int hq;
+  int hkv;
+  int group;               // hq / hkv
+  int page_shift;          // log2(page)
+  float scale_log2;        // log2(e) / sqrt(128)
+};
+
+struct MergeArgs {
+  uint16_t* out;
+  float* lse;
+  const MergeRow* rows;
+  const int32_t* n_rows;
+  const float* part_o;
+  const float* part_lse;
+  int hq;
+};
+
+}  // namespace feattn

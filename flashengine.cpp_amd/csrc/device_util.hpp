@@ -1,0 +1,111 @@
+// Device helpers for gfx950 (CDNA4): element conversions, MFMA wrappers and
+// wavefront (64-lane) exchanges.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace feattn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- element conversions -------------------------------------------------
+// Storage is raw 16-bit; BF16 selects bfloat16 vs IEEE binary16.
+
+template <bool BF16>
+__device__ __forceinline__ float to_f32(uint32_t h16) {
+  if constexpr (BF16) {
+    return __uint_as_float(h16 << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+  }
+}
+
+// Low / high half of a packed pair.
+template <bool BF16>
+__device__ __forceinline__ float lo_f32(uint32_t w) {
+  if constexpr (BF16) return __uint_as_float(w << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+template <bool BF16>
+__device__ __forceinline__ float hi_f32(uint32_t w) {
+  if constexpr (BF16) return __uint_as_float(w & 0xffff0000u);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// fp32 -> 16-bit, round to nearest even.  The bf16 path is written out in
+// integer arithmetic so it is the same function as ATen's CPU conversion
+// (NaN -> 0x7fc0); the fp16 path is the hardware RNE conversion.
+template <bool BF16>
+__device__ __forceinline__ uint32_t from_f32_rne(float f) {
+  if constexpr (BF16) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+  } else {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// Two fp32 -> packed 16-bit pair using the hardware converter (RNE); used for
+// softmax probabilities and attention outputs, where the tolerance, not bit
+// identity, is the contract.
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (BF16) {
+    uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)a);
+    uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)b);
+    return lo | (hi << 16);
+  } else {
+    uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+    uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+    return lo | (hi << 16);
+  }
+}
+
+// ---- MFMA ----------------------------------------------------------------
+// v_mfma_f32_16x16x32_{bf16,f16}.  Operand layout (64 lanes, lane = 16*J + L):
+//   A (16 x 32): lane holds row L, 8 reduction elements selected by (J, e)
+//   B (32 x 16): lane holds column L, the same 8 reduction elements
+//   C (16 x 16): lane holds rows 4*J + r (r = 0..3) of column L
+// Which reduction index (J, e) denotes is the same for A and B, so callers
+// may assign reduction indices to data freely as long as both operands agree.
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// ---- wavefront exchanges -------------------------------------------------
+// Value of lane (lane & ~15) + src within each 16-lane row (ds_swizzle,
+// bit-mask mode: and 0x10, or src).
+template <int SRC>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x10 | (SRC << 5)));
+}
+
+__device__ __forceinline__ float xor16(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (16 << 10) | 0x1f));
+}
+
+__device__ __forceinline__ float xor32(float v) {
+  return __shfl_xor(v, 32, 64);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLn2 = 0.69314718055994530942f;
+
+}  // namespace feattn

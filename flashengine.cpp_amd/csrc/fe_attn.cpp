@@ -1,0 +1,407 @@
+// C ABI of the MI355X attention path (declared in include/fe_attn.h).
+//
+// The plan owns one device arena (sequence table, page table, work lists,
+// counts) plus the split-KV partial buffers, all allocated once at create
+// time from the capacity arguments, like the reference's FlashInfer plan
+// (src/flashinfer_attention.cu:14-27).  prepare() builds the work lists on
+// the host into a pinned mirror of the arena and copies the used ranges on
+// the caller's stream; run() only launches kernels, whose grids depend on
+// the plan capacity in graph mode, so a captured graph stays valid across
+// prepares.
+#include "fe_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "attn_types.hpp"
+#include "planner.hpp"
+
+namespace feattn {
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st);
+hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
+hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
+hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
+                       bool bf16, int max_pos, hipStream_t st);
+hipError_t launch_store(const void* k, const void* v, void* kc, void* vc, const int64_t* slots, int rows, int width,
+                        int64_t cache_slots, hipStream_t st);
+hipError_t launch_rope_append(void* q, const void* k, const void* v, void* kc, void* vc, const int64_t* pos,
+                              const int64_t* slots, const float* cache, int rows, int hq, int hkv, int dim, bool bf16,
+                              int max_pos, int64_t cache_slots, hipStream_t st);
+}  // namespace feattn
+
+using namespace feattn;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FE_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Offsets of the regions inside the metadata arena (same layout on host and device).
+struct Layout {
+  size_t seqs, pages, counts, decode, tile[2], merge[2], total;
+};
+
+Layout make_layout(const PlanShape& sh) {
+  Layout l;
+  size_t off = 0;
+  l.seqs = off;
+  off = align256(off + sizeof(SeqInfo) * sh.max_batch);
+  l.pages = off;
+  off = align256(off + sizeof(int32_t) * (size_t)sh.max_batch * sh.max_pages);
+  l.counts = off;
+  off = align256(off + sizeof(int32_t) * 8);
+  l.decode = off;
+  off = align256(off + sizeof(WorkItem) * sh.item_cap);
+  for (int m = 0; m < 2; ++m) {
+    l.tile[m] = off;
+    off = align256(off + sizeof(WorkItem) * sh.item_cap);
+  }
+  for (int m = 0; m < 2; ++m) {
+    l.merge[m] = off;
+    off = align256(off + sizeof(MergeRow) * sh.partial_cap);
+  }
+  l.total = off;
+  return l;
+}
+
+// counts[] indices
+enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
+
+constexpr size_t kPartialBytes = 64u << 20;  // split-KV workspace (fp32 partial rows)
+
+}  // namespace
+
+struct fe_attn_plan {
+  PlanShape sh;
+  bool bf16 = true;
+  Layout lay{};
+  uint8_t* dev = nullptr;      // metadata arena
+  uint8_t* host = nullptr;     // pinned mirror
+  float* part_o = nullptr;
+  float* part_lse = nullptr;
+  hipEvent_t staged = nullptr;
+  bool staged_pending = false;
+  int device = 0;
+  // state of the last prepare
+  bool prepared = false;
+  bool graph = false;
+  int graph_nc = 0;
+  int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
+  int decode_nc = 4;
+  int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
+};
+
+extern "C" {
+
+const char* fe_attn_last_error(void) { return g_error.c_str(); }
+
+const char* fe_attn_version(void) { return "feattn-hip-gfx950 0.1.0"; }
+
+int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int bf16, int blocks,
+                        fe_attn_plan** plan_out) {
+  if (plan_out == nullptr) return fail(FE_EINVAL, "plan_out is null");
+  *plan_out = nullptr;
+  PlanShape sh;
+  sh.hq = hq;
+  sh.hkv = hkv;
+  sh.dim = dim;
+  sh.page = page;
+  sh.max_batch = max_batch;
+  sh.max_pages = max_pages;
+  sh.blocks = blocks;
+  std::string err;
+  if (validate_shape(sh, err) != FE_OK) return fail(FE_EINVAL, err);
+  const size_t slot_bytes = (size_t)hq * (kHeadDim + 1) * sizeof(float);
+  sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / slot_bytes);
+
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+  sh.num_cus = cus > 0 ? cus : 256;
+
+  auto* p = new fe_attn_plan();
+  p->sh = sh;
+  p->bf16 = bf16 != 0;
+  p->device = dev;
+  p->lay = make_layout(sh);
+  p->grid_decode_cap = sh.num_cus * 2;  // 4 waves per workgroup, 8 resident waves per CU
+  p->grid_tile_cap = sh.num_cus * 2;    // 2 resident 256-thread tile workgroups per CU
+  p->grid_merge_cap = sh.num_cus * 4;
+  auto cleanup = [&](int code, const std::string& msg) {
+    fe_attn_plan_destroy(p);
+    return fail(code, msg);
+  };
+  if (hipMalloc(&p->dev, p->lay.total) != hipSuccess) return cleanup(FE_ENOMEM, "hipMalloc(plan metadata) failed");
+  if (hipHostMalloc(&p->host, p->lay.total, hipHostMallocDefault) != hipSuccess)
+    return cleanup(FE_ENOMEM, "hipHostMalloc(plan staging) failed");
+  std::memset(p->host, 0, p->lay.total);
+  if (hipMalloc(&p->part_o, (size_t)sh.partial_cap * hq * kHeadDim * sizeof(float)) != hipSuccess)
+    return cleanup(FE_ENOMEM, "hipMalloc(split-KV partials) failed");
+  if (hipMalloc(&p->part_lse, (size_t)sh.partial_cap * hq * sizeof(float)) != hipSuccess)
+    return cleanup(FE_ENOMEM, "hipMalloc(split-KV lse) failed");
+  if (hipEventCreateWithFlags(&p->staged, hipEventDisableTiming) != hipSuccess)
+    return cleanup(FE_EDEVICE, "hipEventCreate failed");
+  // Counts start at zero so a run before any prepare does nothing.
+  if (hipMemset(p->dev + p->lay.counts, 0, sizeof(int32_t) * 8) != hipSuccess)
+    return cleanup(FE_EDEVICE, "hipMemset(counts) failed");
+  *plan_out = p;
+  return FE_OK;
+}
+
+int fe_attn_plan_destroy(fe_attn_plan* p) {
+  if (p == nullptr) return FE_OK;
+  if (p->staged_pending) (void)hipEventSynchronize(p->staged);
+  if (p->staged) (void)hipEventDestroy(p->staged);
+  if (p->dev) (void)hipFree(p->dev);
+  if (p->host) (void)hipHostFree(p->host);
+  if (p->part_o) (void)hipFree(p->part_o);
+  if (p->part_lse) (void)hipFree(p->part_lse);
+  delete p;
+  return FE_OK;
+}
+
+int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+                         const int32_t* last, int batch, int rows, int graph, void* stream) {
+  if (p == nullptr) return fail(FE_EINVAL, "plan is null");
+  BuiltPlan bp;
+  std::string err;
+  const int rc = build_plan(p->sh, qo, kv, pages, last, batch, rows, bp, err);
+  if (rc != FE_OK) return fail(rc, err);
+  int nc = bp.decode_nc;
+  if (graph) {
+    // Captured launches bake in the decode column variant; a later prepare
+    // may not need a wider one (the reference refuses layout changes under
+    // graph capture too: src/flashinfer_attention.cu:32).
+    if (p->graph_nc == 0) p->graph_nc = nc;
+    if (nc > p->graph_nc)
+      return fail(FE_EINVAL, "graph plan layout changed: decode rows per sequence grew after capture");
+    nc = p->graph_nc;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // The pinned mirror may still be read by the previous prepare's copies.
+  if (p->staged_pending) {
+    hipError_t e = hipEventSynchronize(p->staged);
+    if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    p->staged_pending = false;
+  }
+  const Layout& l = p->lay;
+  uint8_t* h = p->host;
+  const int npages = batch > 0 ? kv[batch] : 0;
+  std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
+  if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
+  int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
+  cnt[kCntDecode] = (int32_t)bp.decode.size();
+  cnt[kCntTile0] = (int32_t)bp.mode[0].tile.size();
+  cnt[kCntTile1] = (int32_t)bp.mode[1].tile.size();
+  cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
+  cnt[kCntMerge1] = (int32_t)bp.mode[1].merge.size();
+  std::memcpy(h + l.decode, bp.decode.data(), sizeof(WorkItem) * bp.decode.size());
+  for (int m = 0; m < 2; ++m) {
+    std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
+    std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
+  }
+  auto copy = [&](size_t off, size_t bytes) -> hipError_t {
+    if (bytes == 0) return hipSuccess;
+    return hipMemcpyAsync(p->dev + off, h + off, bytes, hipMemcpyHostToDevice, st);
+  };
+  hipError_t e = hipSuccess;
+  if (e == hipSuccess) e = copy(l.seqs, sizeof(SeqInfo) * bp.seqs.size());
+  if (e == hipSuccess) e = copy(l.pages, sizeof(int32_t) * npages);
+  if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
+  if (e == hipSuccess) e = copy(l.decode, sizeof(WorkItem) * bp.decode.size());
+  for (int m = 0; m < 2 && e == hipSuccess; ++m) {
+    e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
+    if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
+  e = hipEventRecord(p->staged, st);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+  p->staged_pending = true;
+  p->prepared = true;
+  p->graph = graph != 0;
+  p->decode_nc = nc;
+  p->n_decode = (int)bp.decode.size();
+  for (int m = 0; m < 2; ++m) {
+    p->n_tile[m] = (int)bp.mode[m].tile.size();
+    p->n_merge[m] = (int)bp.mode[m].merge.size();
+  }
+  return FE_OK;
+}
+
+int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void* v_cache, void* out, float* lse,
+                int causal, void* stream) {
+  if (p == nullptr) return fail(FE_EINVAL, "plan is null");
+  if (!p->prepared) return fail(FE_EINVAL, "attention called before prepare_plan");
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
+    return fail(FE_EINVAL, "null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = causal ? 1 : 0;
+  const int32_t* counts = reinterpret_cast<const int32_t*>(p->dev + p->lay.counts);
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.kc = static_cast<const uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.seqs = reinterpret_cast<const SeqInfo*>(p->dev + p->lay.seqs);
+  a.pages = reinterpret_cast<const int32_t*>(p->dev + p->lay.pages);
+  a.part_o = p->part_o;
+  a.part_lse = p->part_lse;
+  a.hq = p->sh.hq;
+  a.hkv = p->sh.hkv;
+  a.group = p->sh.hq / p->sh.hkv;
+  int shift = 0;
+  while ((1 << shift) < p->sh.page) ++shift;
+  a.page_shift = shift;
+  a.scale_log2 = 1.4426950408889634f / 11.313708498984761f;  // log2(e) / sqrt(128)
+  hipError_t e;
+  if (p->graph || p->n_decode > 0) {
+    AttnArgs d = a;
+    d.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.decode);
+    d.n_items = counts + kCntDecode;
+    const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + 3) / 4);
+    e = launch_decode(d, p->bf16, p->decode_nc, causal ? 1 : 0, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
+  }
+  if (p->graph || p->n_tile[mode] > 0) {
+    AttnArgs t = a;
+    t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.tile[mode]);
+    t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
+    const int grid = p->graph ? p->grid_tile_cap : std::min(p->grid_tile_cap, p->n_tile[mode]);
+    e = launch_tile(t, p->bf16, causal != 0, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "tile kernel launch");
+  }
+  if (p->graph || p->n_merge[mode] > 0) {
+    MergeArgs m{};
+    m.out = static_cast<uint16_t*>(out);
+    m.lse = lse;
+    m.rows = reinterpret_cast<const MergeRow*>(p->dev + p->lay.merge[mode]);
+    m.n_rows = counts + (mode ? kCntMerge1 : kCntMerge0);
+    m.part_o = p->part_o;
+    m.part_lse = p->part_lse;
+    m.hq = p->sh.hq;
+    const int grid = p->graph ? p->grid_merge_cap : std::min(p->grid_merge_cap, p->n_merge[mode]);
+    e = launch_merge(m, p->bf16, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  }
+  return FE_OK;
+}
+
+int fe_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim, int bf16,
+            void* stream, int max_positions) {
+  if (rows < 0 || hq < 0 || hkv < 0) return fail(FE_EINVAL, "rope: negative size");
+  if (dim <= 0 || dim % 16 != 0) return fail(FE_EINVAL, "rope: dim must be a positive multiple of 16");
+  if (rows == 0) return FE_OK;
+  if (q == nullptr || (hkv > 0 && k == nullptr) || pos == nullptr || cache == nullptr)
+    return fail(FE_EINVAL, "rope: null pointer");
+  if (q == k) return fail(FE_EINVAL, "rope: q and k must not alias");
+  const hipError_t e = launch_rope(q, k, pos, cache, rows, hq, hkv, dim, bf16 != 0, max_positions,
+                                   static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "rope kernel launch");
+}
+
+int fe_store(const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* slots, int rows, int width,
+             int bf16, void* stream, int cache_slots) {
+  (void)bf16;  // a 16-bit copy is the same for both types
+  if (rows < 0 || width < 0 || cache_slots < 0) return fail(FE_EINVAL, "store: negative size");
+  if (rows == 0 || width == 0) return FE_OK;
+  if (k == nullptr || v == nullptr || k_cache == nullptr || v_cache == nullptr || slots == nullptr)
+    return fail(FE_EINVAL, "store: null pointer");
+  const hipError_t e =
+      launch_store(k, v, k_cache, v_cache, slots, rows, width, cache_slots, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "store kernel launch");
+}
+
+int fe_rope_append(void* q, const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* pos,
+                   const int64_t* slots, const float* cache, int rows, int hq, int hkv, int dim, int bf16,
+                   int max_positions, int cache_slots, void* stream) {
+  if (rows < 0 || hq < 0 || hkv < 0 || cache_slots < 0) return fail(FE_EINVAL, "rope_append: negative size");
+  if (dim <= 0 || dim % 16 != 0) return fail(FE_EINVAL, "rope_append: dim must be a positive multiple of 16");
+  if (rows == 0) return FE_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || k_cache == nullptr || v_cache == nullptr || pos == nullptr ||
+      slots == nullptr || cache == nullptr)
+    return fail(FE_EINVAL, "rope_append: null pointer");
+  const hipError_t e = launch_rope_append(q, k, v, k_cache, v_cache, pos, slots, cache, rows, hq, hkv, dim,
+                                          bf16 != 0, max_positions, cache_slots, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "rope_append kernel launch");
+}
+
+int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks,
+                          const int32_t* qo, const int32_t* kv, const int32_t* pages, const int32_t* last, int batch,
+                          int rows, int32_t* counts_out) {
+  PlanShape sh;
+  sh.hq = hq;
+  sh.hkv = hkv;
+  sh.dim = dim;
+  sh.page = page;
+  sh.max_batch = max_batch;
+  sh.max_pages = max_pages;
+  sh.blocks = blocks;
+  if (hq > 0) sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * 4));
+  BuiltPlan bp;
+  std::string err;
+  const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
+  if (rc != FE_OK) return fail(rc, err);
+  if (counts_out) {
+    counts_out[0] = (int32_t)bp.decode.size();
+    counts_out[1] = (int32_t)bp.mode[1].tile.size();
+    counts_out[2] = (int32_t)bp.mode[1].merge.size();
+    counts_out[3] = bp.mode[1].partial_rows;
+  }
+  return FE_OK;
+}
+
+int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks, const int32_t* qo,
+                      const int32_t* kv, const int32_t* pages, const int32_t* last, int batch, int rows, int causal,
+                      int32_t* items_out, int cap, int* n_out) {
+  PlanShape sh;
+  sh.hq = hq;
+  sh.hkv = hkv;
+  sh.dim = dim;
+  sh.page = page;
+  sh.max_batch = max_batch;
+  sh.max_pages = max_pages;
+  sh.blocks = blocks;
+  if (hq > 0) sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * 4));
+  BuiltPlan bp;
+  std::string err;
+  const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
+  if (rc != FE_OK) return fail(rc, err);
+  int n = 0;
+  auto emit = [&](int kind, const WorkItem& w) {
+    if (items_out != nullptr && n < cap) {
+      int32_t* o = items_out + 8 * n;
+      o[0] = kind;
+      o[1] = w.seq;
+      o[2] = w.q0;
+      o[3] = w.nq;
+      o[4] = w.kvh;
+      o[5] = w.t0;
+      o[6] = w.t1;
+      o[7] = w.part;
+    }
+    ++n;
+  };
+  for (const WorkItem& w : bp.decode) emit(0, w);
+  for (const WorkItem& w : bp.mode[causal ? 1 : 0].tile) emit(1, w);
+  if (n_out) *n_out = n;
+  return FE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,238 @@
+// Host planner.  Validation mirrors the reference's checks
+// (src/flashinfer_attention.cu:23,30; src/portable_gpu_ops.cpp:28-30) and adds
+// the ones a raw-pointer kernel needs to stay in bounds (page ids, `last`).
+#include "planner.hpp"
+
+#include <algorithm>
+
+#include "fe_attn.h"
+
+namespace feattn {
+
+namespace {
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Sorts by decreasing cost so the longest items start first (LPT order).
+void order_items(std::vector<WorkItem>& items) {
+  std::stable_sort(items.begin(), items.end(),
+                   [](const WorkItem& x, const WorkItem& y) { return x.cost > y.cost; });
+}
+
+}  // namespace
+
+int validate_shape(const PlanShape& sh, std::string& err) {
+  if (sh.dim != kHeadDim) {
+    err = "attention supports head_dim 128 only (got " + std::to_string(sh.dim) + ")";
+    return FE_EINVAL;
+  }
+  if (sh.hq <= 0 || sh.hkv <= 0 || sh.hq % sh.hkv != 0) {
+    err = "hq must be a positive multiple of hkv";
+    return FE_EINVAL;
+  }
+  if (sh.hq / sh.hkv > kTileCols) {
+    err = "GQA group larger than 128 query heads per kv head";
+    return FE_EINVAL;
+  }
+  if (!is_pow2(sh.page) || sh.page < 16) {
+    err = "page size must be a power of two >= 16";
+    return FE_EINVAL;
+  }
+  if (sh.max_batch <= 0 || sh.max_pages <= 0 || sh.blocks < 0) {
+    err = "max_batch and max_pages must be positive, blocks non-negative";
+    return FE_EINVAL;
+  }
+  return FE_OK;
+}
+
+int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+               const int32_t* last, int batch, int rows, BuiltPlan& out, std::string& err) {
+  int rc = validate_shape(sh, err);
+  if (rc != FE_OK) return rc;
+  if (batch < 0 || rows < 0) {
+    err = "negative batch or rows";
+    return FE_EINVAL;
+  }
+  if (batch > sh.max_batch) {
+    err = "attention metadata exceeds capacity: batch " + std::to_string(batch) + " > max_batch " +
+          std::to_string(sh.max_batch);
+    return FE_ECAPACITY;
+  }
+  out = BuiltPlan();
+  if (batch > 0 && (qo == nullptr || kv == nullptr || last == nullptr)) {
+    err = "null metadata pointer";
+    return FE_EINVAL;
+  }
+  const int64_t max_context = (int64_t)(sh.max_pages - 1) * sh.page;
+  if (batch > 0) {
+    if (qo[0] < 0 || kv[0] < 0) {
+      err = "qo[0] and kv[0] must be non-negative";
+      return FE_EINVAL;
+    }
+    if ((int64_t)kv[batch] > (int64_t)sh.max_batch * sh.max_pages) {
+      err = "attention metadata exceeds capacity: kv[batch] > max_batch * max_pages";
+      return FE_ECAPACITY;
+    }
+    if (kv[batch] > 0 && pages == nullptr) {
+      err = "null page table";
+      return FE_EINVAL;
+    }
+  }
+  out.seqs.resize(batch);
+  for (int b = 0; b < batch; ++b) {
+    const int np = kv[b + 1] - kv[b];
+    const int ql = qo[b + 1] - qo[b];
+    if (np < 1 || ql < 0) {
+      err = "sequence " + std::to_string(b) + ": qo/kv offsets must be non-decreasing with >= 1 page";
+      return FE_EINVAL;
+    }
+    if (last[b] < 1 || last[b] > sh.page) {
+      err = "sequence " + std::to_string(b) + ": last must be in [1, page]";
+      return FE_EINVAL;
+    }
+    const int64_t len = (int64_t)(np - 1) * sh.page + last[b];
+    if (len < ql || len > max_context) {
+      err = "attention context out of range for sequence " + std::to_string(b) + " (len " + std::to_string(len) +
+            ", query rows " + std::to_string(ql) + ", max_context " + std::to_string(max_context) + ")";
+      return FE_EINVAL;
+    }
+    for (int i = kv[b]; i < kv[b + 1]; ++i) {
+      if (pages[i] < 0 || pages[i] > sh.blocks) {
+        err = "page id " + std::to_string(pages[i]) + " outside [0, blocks]";
+        return FE_EINVAL;
+      }
+    }
+    out.seqs[b] = SeqInfo{qo[b], ql, (int32_t)len, kv[b]};
+  }
+  if (batch > 0 && qo[batch] > rows) {
+    err = "qo[batch] exceeds rows";
+    return FE_EINVAL;
+  }
+
+  const int G = sh.hq / sh.hkv;
+  const int slot_budget = sh.partial_cap;
+
+  // ---- decode items: sequences whose (rows x group) fit one MFMA column block.
+  int64_t decode_tokens = 0;
+  int max_cols = 0;
+  for (int b = 0; b < batch; ++b) {
+    const SeqInfo& s = out.seqs[b];
+    if (s.qlen > 0 && s.qlen * G <= kDecodeCols) {
+      decode_tokens += (int64_t)s.len * sh.hkv;
+      max_cols = std::max(max_cols, s.qlen * G);
+    }
+  }
+  out.decode_nc = max_cols <= 4 ? 4 : max_cols <= 8 ? 8 : 16;
+  if (decode_tokens > 0) {
+    // About 16 work items per compute unit (4 resident waves each, several
+    // rounds) with at least 128 tokens per item; splits cost one fp32 partial
+    // row per query row, so the chunk grows until the partials fit.
+    const int64_t target = (int64_t)sh.num_cus * 16;
+    int chunk = (int)std::min<int64_t>(1 << 20, (decode_tokens + target - 1) / target);
+    chunk = std::max(128, round_up(chunk, 64));
+    for (;;) {
+      int slots = 0;
+      size_t n_items = 0;
+      for (int b = 0; b < batch; ++b) {
+        const SeqInfo& s = out.seqs[b];
+        if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
+        const int ns = ceil_div(s.len, chunk);
+        if (ns > 1) slots += ns * s.qlen;
+        n_items += (size_t)ns * sh.hkv;
+      }
+      if (slots <= slot_budget && n_items <= (size_t)sh.item_cap) break;
+      if (chunk >= (1 << 22)) {
+        err = "attention metadata exceeds capacity: decode work list";
+        return FE_ECAPACITY;
+      }
+      chunk *= 2;
+    }
+    for (int b = 0; b < batch; ++b) {
+      const SeqInfo& s = out.seqs[b];
+      if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
+      const int ns = ceil_div(s.len, chunk);
+      int base = -1;
+      if (ns > 1) {
+        base = out.decode_partials;
+        out.decode_partials += ns * s.qlen;
+        for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, ns, s.qlen});
+      }
+      for (int sp = 0; sp < ns; ++sp) {
+        const int t0 = sp * chunk;
+        const int t1 = std::min<int>(s.len, t0 + chunk);
+        for (int h = 0; h < sh.hkv; ++h)
+          out.decode.push_back(WorkItem{b, s.qo, s.qlen, h, t0, t1, base < 0 ? -1 : base + sp * s.qlen, t1 - t0});
+      }
+    }
+    order_items(out.decode);
+  }
+
+  // ---- tile items, per mask mode.
+  const int qr = kTileCols / G;  // query rows per tile item
+  for (int causal = 0; causal < 2; ++causal) {
+    ModeLists& ml = out.mode[causal];
+    ml.partial_rows = out.decode_partials;
+    // (q tile, kv head) pairs before splitting, to size the split factor.
+    int64_t pairs = 0;
+    for (int b = 0; b < batch; ++b) {
+      const SeqInfo& s = out.seqs[b];
+      if (s.qlen * G > kDecodeCols) pairs += (int64_t)ceil_div(s.qlen, qr) * sh.hkv;
+    }
+    if (pairs == 0) continue;
+    // Aim for >= 2 resident workgroups per compute unit; never split below 256 tokens.
+    int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 2 + pairs - 1) / pairs);
+    for (;;) {
+      ml.tile.clear();
+      ml.merge.clear();
+      ml.partial_rows = out.decode_partials;
+      for (int b = 0; b < batch; ++b) {
+        const SeqInfo& s = out.seqs[b];
+        if (s.qlen * G <= kDecodeCols) continue;
+        for (int i0 = 0; i0 < s.qlen; i0 += qr) {
+          const int nq = std::min(qr, s.qlen - i0);
+          const int extent = causal ? std::min(s.len, s.len - s.qlen + i0 + nq) : s.len;
+          int ns = std::max(1, std::min(want, extent / 256));
+          int chunk = round_up(ceil_div(extent, ns), kTileTokens);
+          ns = ceil_div(extent, chunk);
+          int base = -1;
+          if (ns > 1) {
+            base = ml.partial_rows;
+            ml.partial_rows += ns * nq;
+            for (int r = 0; r < nq; ++r) ml.merge.push_back(MergeRow{s.qo + i0 + r, base + r, ns, nq});
+          }
+          for (int sp = 0; sp < ns; ++sp) {
+            const int t0 = sp * chunk;
+            const int t1 = std::min(extent, t0 + chunk);
+            // Cost ~ MFMA work: visible tokens times columns (the causal
+            // diagonal tile counted in full).
+            const int cost = (t1 - t0) / 16 * nq * G / 16 + 1;
+            for (int h = 0; h < sh.hkv; ++h)
+              ml.tile.push_back(WorkItem{b, s.qo + i0, nq, h, t0, t1, base < 0 ? -1 : base + sp * nq, cost});
+          }
+        }
+      }
+      if (ml.partial_rows <= slot_budget && ml.tile.size() <= (size_t)sh.item_cap) break;
+      if (want == 1) {
+        err = "attention metadata exceeds capacity: tile work list (" + std::to_string(ml.tile.size()) + " items)";
+        return FE_ECAPACITY;
+      }
+      want = std::max(1, want / 2);
+    }
+    order_items(ml.tile);
+  }
+  for (int causal = 0; causal < 2; ++causal) {
+    std::vector<MergeRow>& m = out.mode[causal].merge;
+    m.insert(m.begin(), out.decode_merge.begin(), out.decode_merge.end());
+    if (m.size() > (size_t)slot_budget) {
+      err = "attention metadata exceeds capacity: merge rows";
+      return FE_ECAPACITY;
+    }
+  }
+  return FE_OK;
+}
+
+}  // namespace feattn

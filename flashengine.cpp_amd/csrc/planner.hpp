@@ -1,0 +1,47 @@
+// Host-side planner: validates the reference's CSR metadata and turns it into
+// decode / tile / merge work lists.  Pure host code (no HIP calls), so it is
+// also exercised by the CPU tests through fe_attn_plan_describe / _dump.
+#pragma once
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "attn_types.hpp"
+
+namespace feattn {
+
+struct PlanShape {
+  int hq = 0;
+  int hkv = 0;
+  int dim = 0;
+  int page = 0;
+  int max_batch = 0;
+  int max_pages = 0;
+  int blocks = 0;
+  int num_cus = 256;        // compute units on the device (sizes split-KV)
+  int item_cap = 1 << 16;   // work items per list
+  int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
+};
+
+struct ModeLists {
+  std::vector<WorkItem> tile;
+  std::vector<MergeRow> merge;
+  int partial_rows = 0;  // decode partials followed by this mode's tile partials
+};
+
+struct BuiltPlan {
+  std::vector<SeqInfo> seqs;
+  std::vector<WorkItem> decode;  // identical for both masks (end-aligned causal)
+  int decode_partials = 0;
+  std::vector<MergeRow> decode_merge;
+  int decode_nc = 4;             // 4, 8 or 16 columns per decode item
+  ModeLists mode[2];             // [0] full (non-causal), [1] causal
+};
+
+// Returns 0 (FE_OK) or a negative FE_E* code with `err` set.
+int validate_shape(const PlanShape& sh, std::string& err);
+int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+               const int32_t* last, int batch, int rows, BuiltPlan& out, std::string& err);
+
+}  // namespace feattn

@@ -1,0 +1,194 @@
+"""ctypes binding of libfeattn.so (the C ABI declared in include/fe_attn.h).
+
+This is plumbing for the tests, the smoke check and the benchmark: torch
+provides device memory and the current HIP stream, every computation runs in
+the library's HIP kernels.  There is no fallback: if the library is missing,
+:func:`lib` raises.
+
+The functions mirror the reference's ``fe::cuda`` boundary
+(include/fe/native_cuda.hpp:6-14): same names, same argument meaning, and a
+failed call raises ``RuntimeError`` with the library's message, as the
+reference's ``check()`` throws ``std::runtime_error``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libfeattn.so")
+
+FE_OK = 0
+FE_EINVAL = -1
+FE_ECAPACITY = -2
+FE_EDEVICE = -3
+FE_ENOMEM = -4
+
+# Every extern "C" symbol of include/fe_attn.h.
+C_SYMBOLS = (
+    "fe_attn_plan_create",
+    "fe_attn_plan_destroy",
+    "fe_attn_plan_prepare",
+    "fe_attn_run",
+    "fe_rope",
+    "fe_store",
+    "fe_rope_append",
+    "fe_attn_last_error",
+    "fe_attn_plan_describe",
+    "fe_attn_plan_dump",
+    "fe_attn_version",
+)
+
+_LIB: Optional[ctypes.CDLL] = None
+
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libfeattn.so once.  torch is imported first so that the library
+    binds to the HIP runtime torch already loaded (same SONAME)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `make -C flashengine.cpp_amd` "
+            "or __graft_entry__.build() first")
+    import torch  # noqa: F401  (HIP runtime first)
+
+    L = ctypes.CDLL(LIB_PATH)
+    L.fe_attn_last_error.restype = ctypes.c_char_p
+    L.fe_attn_last_error.argtypes = []
+    L.fe_attn_version.restype = ctypes.c_char_p
+    L.fe_attn_version.argtypes = []
+    L.fe_attn_plan_create.argtypes = [_int] * 8 + [ctypes.POINTER(_vp)]
+    L.fe_attn_plan_destroy.argtypes = [_vp]
+    L.fe_attn_plan_prepare.argtypes = [_vp, _i32p, _i32p, _i32p, _i32p, _int, _int, _int, _vp]
+    L.fe_attn_run.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
+    L.fe_rope.argtypes = [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _int]
+    L.fe_store.argtypes = [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _int]
+    L.fe_rope_append.argtypes = [_vp] * 8 + [_int] * 7 + [_vp]
+    L.fe_attn_plan_describe.argtypes = [_int] * 7 + [_i32p] * 4 + [_int, _int, _i32p]
+    L.fe_attn_plan_dump.argtypes = [_int] * 7 + [_i32p] * 4 + [_int, _int, _int, _i32p, _int,
+                                                             ctypes.POINTER(_int)]
+    for name in C_SYMBOLS:
+        getattr(L, name).restype = ctypes.c_char_p if name in (
+            "fe_attn_last_error", "fe_attn_version") else _int
+    _LIB = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != FE_OK:
+        msg = lib().fe_attn_last_error().decode(errors="replace")
+        raise RuntimeError(f"feattn error {rc}: {msg}")
+
+
+def _i32(values: Sequence[int]):
+    arr = (ctypes.c_int32 * max(1, len(values)))(*values)
+    return arr
+
+
+def _stream(stream) -> int:
+    import torch
+
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class Plan:
+    """Owning wrapper of ``fe_attn_plan`` (reference: fe::cuda::AttentionPlan,
+    created with create_plan's arguments, native_cuda.hpp:7)."""
+
+    def __init__(self, hq: int, hkv: int, dim: int, page: int, max_batch: int,
+                 max_pages: int, bf16: bool, blocks: int):
+        self.hq, self.hkv, self.dim, self.page = hq, hkv, dim, page
+        self.max_batch, self.max_pages, self.bf16, self.blocks = max_batch, max_pages, bf16, blocks
+        handle = _vp()
+        _check(lib().fe_attn_plan_create(hq, hkv, dim, page, max_batch, max_pages,
+                                         int(bool(bf16)), blocks, ctypes.byref(handle)))
+        self._h = handle
+        self.rows = 0
+
+    def prepare(self, qo: Sequence[int], kv: Sequence[int], pages: Sequence[int],
+                last: Sequence[int], batch: int, rows: int, graph: bool = False,
+                stream=None) -> None:
+        """fe::cuda::prepare_plan (native_cuda.hpp:9): host CSR metadata."""
+        _check(lib().fe_attn_plan_prepare(self._h, _i32(qo), _i32(kv), _i32(pages), _i32(last),
+                                          batch, rows, int(bool(graph)), _stream(stream)))
+        self.rows = rows
+
+    def run(self, q, k_cache, v_cache, out, causal: bool = True, lse=None, stream=None) -> None:
+        """fe::cuda::attention (native_cuda.hpp:10) plus the optional LSE output."""
+        _check(lib().fe_attn_run(self._h, _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                 _ptr(lse), int(bool(causal)), _stream(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().fe_attn_plan_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rope(q, k, pos, cache, rows: int, hq: int, hkv: int, dim: int, bf16: bool,
+         max_positions: int, stream=None) -> None:
+    """fe::cuda::rope (native_cuda.hpp:13), in place on q and k."""
+    _check(lib().fe_rope(_ptr(q), _ptr(k), _ptr(pos), _ptr(cache), rows, hq, hkv, dim,
+                         int(bool(bf16)), _stream(stream), max_positions))
+
+
+def store(k, v, k_cache, v_cache, slots, rows: int, width: int, bf16: bool,
+          cache_slots: int, stream=None) -> None:
+    """fe::cuda::store (native_cuda.hpp:14): slot < 0 rows are skipped."""
+    _check(lib().fe_store(_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), _ptr(slots), rows,
+                          width, int(bool(bf16)), _stream(stream), cache_slots))
+
+
+def rope_append(q, k, v, k_cache, v_cache, pos, slots, cache, rows: int, hq: int, hkv: int,
+                dim: int, bf16: bool, max_positions: int, cache_slots: int, stream=None) -> None:
+    """Fused rope + store of the new tokens (q rotated in place)."""
+    _check(lib().fe_rope_append(_ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), _ptr(pos),
+                                _ptr(slots), _ptr(cache), rows, hq, hkv, dim, int(bool(bf16)),
+                                max_positions, cache_slots, _stream(stream)))
+
+
+def describe(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, last, batch, rows):
+    """Host-only planner counts: (decode items, causal tile items, merge rows, partial rows)."""
+    out = (ctypes.c_int32 * 4)()
+    _check(lib().fe_attn_plan_describe(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
+                                       _i32(kv), _i32(pages), _i32(last), batch, rows, out))
+    return tuple(out)
+
+
+def dump(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, last, batch, rows,
+         causal: bool):
+    """Host-only planner work list: list of (kind, seq, q0, nq, kvh, t0, t1, part)."""
+    n = _int()
+    _check(lib().fe_attn_plan_dump(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
+                                   _i32(kv), _i32(pages), _i32(last), batch, rows, int(causal),
+                                   None, 0, ctypes.byref(n)))
+    buf = (ctypes.c_int32 * (8 * max(1, n.value)))()
+    _check(lib().fe_attn_plan_dump(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
+                                   _i32(kv), _i32(pages), _i32(last), batch, rows, int(causal),
+                                   buf, n.value, ctypes.byref(n)))
+    return [tuple(buf[8 * i:8 * i + 8]) for i in range(n.value)]
+
+
+def version() -> str:
+    return lib().fe_attn_version().decode()

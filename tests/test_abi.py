@@ -1,0 +1,69 @@
+"""The C-ABI library loads without a GPU and exports every symbol the
+headers declare (no compute calls here)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import feattn
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fe_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_matches_binding_list():
+    names = header_functions(os.path.join(ROOT, "include", "fe_attn.h"))
+    assert names == sorted(feattn.C_SYMBOLS)
+
+
+def test_library_exports_every_c_symbol():
+    lib = feattn.lib()
+    for name in header_functions(os.path.join(ROOT, "include", "fe_attn.h")):
+        assert hasattr(lib, name), name
+    assert feattn.version().startswith("feattn-hip-gfx950")
+
+
+def test_library_exports_reference_namespace():
+    """fe::cuda:: symbols with the reference's exact parameter lists
+    (include/fe/native_cuda.hpp:7-14), so cuda_model.cpp can link unchanged."""
+    out = subprocess.run(["nm", "-DC", feattn.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    want = [
+        "fe::cuda::create_plan(int, int, int, int, int, int, bool, int)",
+        "fe::cuda::destroy_plan(fe::cuda::AttentionPlan*)",
+        "fe::cuda::prepare_plan(fe::cuda::AttentionPlan*, int const*, int const*, int const*, "
+        "int const*, int, int, bool, void*)",
+        "fe::cuda::attention(fe::cuda::AttentionPlan*, void*, void*, void*, void*, bool, void*)",
+        "fe::cuda::rope(void*, void*, long const*, float const*, int, int, int, int, bool, void*, int)",
+        "fe::cuda::store(void const*, void const*, void*, void*, long const*, int, int, bool, void*, int)",
+    ]
+    for w in want:
+        assert w in out, w
+
+
+def test_library_links_only_the_hip_runtime():
+    """No torch or CUDA in the product library's dependencies."""
+    out = subprocess.run(["readelf", "-d", feattn.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    needed = re.findall(r"Shared library: \[(.+?)\]", out)
+    assert any(n.startswith("libamdhip64") for n in needed)
+    assert not any("torch" in n or "cuda" in n or "c10" in n for n in needed), needed
+
+
+def test_error_reporting_without_device():
+    """create rejects a bad head size before touching the device."""
+    lib = feattn.lib()
+    h = ctypes.c_void_p()
+    rc = lib.fe_attn_plan_create(32, 8, 64, 16, 4, 4, 1, 16, ctypes.byref(h))
+    assert rc == feattn.FE_EINVAL
+    assert b"128" in lib.fe_attn_last_error()
+    rc = lib.fe_attn_plan_create(32, 8, 128, 24, 4, 4, 1, 16, ctypes.byref(h))
+    assert rc == feattn.FE_EINVAL and b"page" in lib.fe_attn_last_error()
+    rc = lib.fe_attn_plan_create(30, 8, 128, 16, 4, 4, 1, 16, ctypes.byref(h))
+    assert rc == feattn.FE_EINVAL

@@ -1,0 +1,122 @@
+"""Host planner (no device): validation mirrors the reference's checks and
+the work lists cover every visible (row, head, token) exactly once."""
+
+import numpy as np
+import pytest
+
+import feattn
+from feattn import workloads as W
+
+
+def plan_args(b, max_pages=None, max_batch=None):
+    return (b.hq, b.hkv, 128, b.page, max_batch or max(1, b.batch), max_pages or b.max_pages(),
+            b.blocks, b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+
+
+def coverage(b, causal):
+    """Counts, per (row, kv head, token), how often a work item covers it
+    where the token is visible to the row."""
+    items = feattn.dump(*plan_args(b), causal=causal)
+    lens = b.lens
+    seq_of_row = np.zeros(b.rows, np.int64)
+    for s in range(b.batch):
+        seq_of_row[b.qo[s]:b.qo[s + 1]] = s
+    maxlen = max(lens)
+    cnt = np.zeros((b.rows, b.hkv, maxlen), np.int32)
+    for kind, seq, q0, nq, kvh, t0, t1, part in items:
+        assert 0 <= t0 < t1 <= lens[seq]
+        assert t0 % 16 == 0
+        if kind == 1:
+            assert t0 % 64 == 0
+            assert nq * b.group <= 128
+        else:
+            assert nq * b.group <= 16
+        for r in range(q0, q0 + nq):
+            assert seq_of_row[r] == seq
+            i = r - b.qo[seq]
+            lim = lens[seq] - b.qlens[seq] + i if causal else lens[seq] - 1
+            hi = min(t1, lim + 1)
+            if hi > t0:
+                cnt[r, kvh, t0:hi] += 1
+    for r in range(b.rows):
+        s = seq_of_row[r]
+        i = r - b.qo[s]
+        lim = lens[s] - b.qlens[s] + i if causal else lens[s] - 1
+        assert (cnt[r, :, :lim + 1] == 1).all(), (r, causal)
+        assert (cnt[r, :, lim + 1:] == 0).all()
+    return items
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_coverage_mixed_ragged(causal):
+    b = W.make_batch(32, 4, starts=[0, 5, 700, 100, 4000, 33], qlens=[1, 3, 1, 200, 1, 70],
+                     seed=7, extra_pages=2)
+    coverage(b, causal)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_coverage_prefill_and_dflash(causal):
+    coverage(W.make_batch(32, 8, starts=[0, 1000, 17], qlens=[300, 64, 129], seed=3), causal)
+    coverage(W.make_batch(32, 8, starts=[2048, 3000], qlens=[16, 16], seed=4), causal)
+
+
+def test_coverage_gqa_variants():
+    for hq, hkv in ((8, 8), (16, 8), (40, 8), (64, 4)):
+        b = W.make_batch(hq, hkv, starts=[10, 300], qlens=[1, 40], seed=hq)
+        coverage(b, True)
+
+
+def test_split_kv_produces_merges():
+    b = W.long_decode(batch=4, ctx=32768)
+    counts = feattn.describe(*plan_args(b))
+    assert counts[0] > 4 * 8          # split
+    assert counts[2] == 4             # one merge row per sequence
+    items = coverage(b, True)
+    assert all(it[7] >= 0 for it in items)
+
+
+def test_decode_config_layout():
+    b = W.qwen3_8b_decode()
+    d, t, m, p = feattn.describe(*plan_args(b))
+    assert t == 0 and d >= 1024 and m <= b.batch
+
+
+@pytest.mark.parametrize("mutate,code", [
+    ("batch_over", feattn.FE_ECAPACITY),
+    ("last_zero", feattn.FE_EINVAL),
+    ("last_big", feattn.FE_EINVAL),
+    ("page_oob", feattn.FE_EINVAL),
+    ("len_lt_qlen", feattn.FE_EINVAL),
+    ("len_gt_max_context", feattn.FE_EINVAL),
+    ("rows_short", feattn.FE_EINVAL),
+])
+def test_validation(mutate, code):
+    b = W.make_batch(32, 8, starts=[40, 3], qlens=[1, 5], seed=1)
+    qo, kv, pages, last = list(b.qo), list(b.kv), list(b.pages), list(b.last)
+    max_batch, max_pages, rows = 2, b.max_pages(), b.rows
+    if mutate == "batch_over":
+        max_batch = 1
+    elif mutate == "last_zero":
+        last[0] = 0
+    elif mutate == "last_big":
+        last[1] = 17
+    elif mutate == "page_oob":
+        pages[0] = b.blocks + 1
+    elif mutate == "len_lt_qlen":
+        qo[2] = qo[1] + 9  # 9 query rows for an 8-token sequence
+        rows = qo[2]
+    elif mutate == "len_gt_max_context":
+        max_pages = 2  # max_context 16 < 41
+    elif mutate == "rows_short":
+        rows = b.rows - 1
+    with pytest.raises(RuntimeError) as e:
+        feattn.describe(32, 8, 128, 16, max_batch, max_pages, b.blocks, qo, kv, pages, last,
+                        b.batch, rows)
+    assert f"error {code}" in str(e.value)
+
+
+def test_empty_batch_and_zero_row_sequence():
+    assert feattn.describe(32, 8, 128, 16, 4, 4, 10, [0], [0], [], [], 0, 0) == (0, 0, 0, 0)
+    b = W.make_batch(32, 8, starts=[20, 7], qlens=[0, 2], seed=2)
+    items = coverage(b, True)
+    assert all(it[1] == 1 for it in items)
