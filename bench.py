@@ -181,6 +181,20 @@ def secondary(dev):
     return res
 
 
+def copy_calibration(dev, mib=1024):
+    """A plain device copy of known size (read + write of `mib` MiB), timed:
+    the practical bandwidth reference, and the kernel whose FETCH_SIZE /
+    WRITE_SIZE counters calibrate the attention kernels' traffic."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = event_time_ms(lambda i: dst.copy_(src), 10, 2)
+    del src, dst
+    return {"bytes_per_copy": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / ms / 1e6, 1)}
+
+
 def cpu_baseline(b):
     """Oracle (LibTorch-CPU restatement of the reference ATen attention) on
     the full decode batch: median of 3 after 1 warmup."""
@@ -241,6 +255,8 @@ def main():
     gbs = nbytes / ms / 1e6
     log(f"decode: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
     sec = {} if args.no_secondary else secondary(dev)
+    sec["copy_calibration"] = copy_calibration(dev)
+    log("copy", sec["copy_calibration"])
     cpu = None if args.no_cpu else cpu_baseline(b)
 
     line = {

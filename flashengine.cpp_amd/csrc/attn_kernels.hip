@@ -16,7 +16,8 @@
 //    LDS; each wavefront owns 32 (query row, head) columns and computes
 //    S^T = K Q^T and O^T = V^T P^T on the bf16/fp16 MFMA with fp32
 //    accumulation (chunked prefill, DFlash blocks, verify rows).
-//  * attn_merge_kernel: combines split-KV partials by their log-sum-exp.
+//  * attn_merge_kernel: combines split-KV partials by their log-sum-exp, one
+//    wavefront per (query row, head) with every split's loads in flight.
 #include <type_traits>
 
 #include "attn_types.hpp"
@@ -36,19 +37,97 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Reads of plan metadata (work items, sequence table, page table) through
+// the constant address space: these buffers are not written while a kernel
+// runs, so wave-uniform indices become scalar loads.
+typedef const __attribute__((address_space(4))) int32_t* const_i32p;
+
+__device__ __forceinline__ int32_t ldc(const int32_t* p, size_t i) { return ((const_i32p)p)[i]; }
+
+__device__ __forceinline__ WorkItem ldc_item(const WorkItem* items, int i) {
+  const int32_t* p = reinterpret_cast<const int32_t*>(items + i);
+  return WorkItem{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3), ldc(p, 4), ldc(p, 5), ldc(p, 6), ldc(p, 7)};
+}
+
+__device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
+  const int32_t* p = reinterpret_cast<const int32_t*>(seqs + i);
+  return SeqInfo{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3)};
+}
+
 // ===========================================================================
 // Decode kernel
 // ===========================================================================
-// Lane = 16*J + L.  For a 16-token block starting at token `tok`:
-//   K operand: lane loads token tok+L, elements 32*s + 8*J .. +8 for k-step s
-//              (each instruction reads 64 contiguous bytes of 16 token rows);
-//   Q operand: lane holds column L, the same elements;
-//   S^T (C):   lane holds tokens tok + 4*J + r (r = 0..3) of column L;
-//   V:         lane group J handles tokens tok + 4*J + r, lane L owns the
-//              head dims 8*L .. 8*L+7 (one 16-byte load per token row,
-//              16 lanes cover the 256-byte row).
-template <bool BF16, int NC, int NB>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, int causal) {
+// One wavefront per work item of <= 16 (query row, head) columns; WAVES
+// wavefronts per workgroup take consecutive items, which the planner orders
+// (sequence, chunk, kv head), so a workgroup streams whole pages of the cache.
+//
+// K and V of each 16-token block are copied HBM -> LDS by direct-to-LDS loads
+// (global_load_lds_dwordx4: lane i of an instruction lands at LDS base + 16 i)
+// into a two-stage ring private to the wavefront; the next block's copy is in
+// flight while the current one is computed.  Every copy instruction moves
+// four whole 256-byte token rows.  Inside a stage, the 16-byte chunk c of
+// token row t is stored at chunk position c ^ t (K) or c ^ (2t mod 16) (V),
+// which makes both operand reads below free of LDS bank conflicts.
+//
+// Lane = 16*J + L.  Per block:
+//   S^T = K Q^T:  A = K rows (lane: token L, dims 32s+8J..+8, ds_read_b128),
+//                 B = Q^T (lane: column L, the same dims), 4 x 16x16x32 MFMA;
+//                 C: lane holds tokens 4J+r (r = 0..3) of column L.
+//   O^T += V^T P^T: A = V^T (lane: dim 16db+L, tokens 4J..4J+3, one
+//                 ds_read_b64_tr_b16), B = P^T (lane: column L, tokens
+//                 4J..4J+3 = its own S^T values), 8 x 16x16x16 MFMA;
+//                 C: lane holds dims 16db+4J+r of column L.
+// Softmax statistics are per column, i.e. per lane (reduced over J).
+constexpr int kDecStage = 8192;    // LDS bytes per 16-token block (K then V)
+constexpr int kDecStages = 2;
+
+__device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gaddr), "s"(lds_addr)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                      0, 0, 0);
+  } else {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                                 0, 0);
+  }
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t lds_addr) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)lds_addr);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ __forceinline__ u32x4 lds_read16(uint32_t lds_addr) {
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  return *(lds_u32x4*)(uintptr_t)lds_addr;
+}
+
+template <bool BF16, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int causal) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int J = lane >> 4;
   const int L = lane & 15;
@@ -57,14 +136,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, int causal
   const int G = a.group;
   const int pshift = a.page_shift;
   const int pmask = (1 << pshift) - 1;
+  const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * kDecStages * kDecStage);
 
-  for (int it = blockIdx.x * 4 + wave; it < n_items; it += gridDim.x * 4) {
-    const WorkItem w = a.items[it];
-    const SeqInfo s = a.seqs[uniform(w.seq)];
-    const int kvh = uniform(w.kvh);
-    const int t0 = uniform(w.t0);
-    const int t1 = uniform(w.t1);
-    const int ncols = uniform(w.nq) * G;
+  // Per-lane pieces of the copy and read addresses (fixed for the kernel).
+  // Copy instruction r, lane i = 16*J + L: token row 4r + J, chunk position L;
+  // the global chunk is L ^ row (K) or L ^ (2 row mod 16) (V).
+  int k_goff[4], v_goff[4];
+  const int row_bytes = a.hkv * kHeadDim * 2;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 4 * r + J;
+    k_goff[r] = t * row_bytes + 16 * (L ^ t);
+    v_goff[r] = t * row_bytes + 16 * (L ^ ((2 * t) & 15));
+  }
+  // K operand chunk position for k-step s: token L, chunk (4s + J) ^ L.
+  uint32_t k_lds[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) k_lds[s] = (uint32_t)(16 * (16 * L + (((4 * s + J) ^ L) & 15)));
+  // V^T operand for dim block db: lane (J, L = 4k + m) points at token 4J + k,
+  // dims 16 db + 4m .. +3 (chunk 2 db + m/2, half m%2).
+  uint32_t v_lds[8];
+  {
+    const int k = L >> 2, m = L & 3, t = 4 * J + k;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int c = 2 * db + (m >> 1);
+      v_lds[db] = (uint32_t)(4096 + 16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
+    }
+  }
+
+  for (int it = blockIdx.x * WAVES + wave; it < n_items; it += gridDim.x * WAVES) {
+    const WorkItem w = ldc_item(a.items, it);
+    const SeqInfo s = ldc_seq(a.seqs, w.seq);
+    const int kvh = w.kvh;
+    const int t0 = w.t0;
+    const int t1 = w.t1;
+    const int ncols = w.nq * G;
 
     const bool col_ok = L < ncols;
     const int crow = w.q0 + (col_ok ? L / G : 0);
@@ -75,70 +182,79 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, int causal
       lim = min(lim, t1 - 1);
     }
 
+    const char* kbase = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
+    const char* vbase = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
+    auto issue = [&](int tok, int pg, int stage) {
+      const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
+      const uint32_t st = ring + (uint32_t)(stage * kDecStage);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(kbase + blk + k_goff[r], st + 1024 * r);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(vbase + blk + v_goff[r], st + 4096 + 1024 * r);
+    };
+
+    // Item start: the first block's copy (its page id by a scalar load), the
+    // item's page ids (one per lane, in windows of 64 pages) and the Q^T
+    // operand (column L) are all in flight before the one wait for them.  The empty asm then hands the registers on as plain
+    // values, so no wait for them lands inside the token loop, where the
+    // next block's copy is in flight.
+    wait_lds();  // earlier reads of the ring are complete before it is refilled
+    issue(t0, ldc(a.pages, s.page_off + (t0 >> pshift)), 0);
+    const int plast = (t1 - 1) >> pshift;
+    int pwin = t0 >> pshift;
+    auto window = [&](int first) {
+      const int idx = first + lane;
+      return idx <= plast ? a.pages[s.page_off + idx] : 0;
+    };
+    int pgv = window(pwin);
     u32x4 qf[4];
     {
       const uint16_t* qp = a.q + ((size_t)crow * a.hq + chead) * kHeadDim + 8 * J;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) qf[k] = col_ok ? ld16(qp + 32 * k) : u32x4{0u, 0u, 0u, 0u};
+      for (int k = 0; k < 4; ++k) qf[k] = ld16(qp + 32 * k);
+      asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(pgv));
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
     }
+    auto page_of = [&](int tok) {
+      if ((tok >> pshift) - pwin >= 64) {  // next window (long items only)
+        pwin += 64;
+        pgv = window(pwin);
+        asm volatile("" : "+v"(pgv));
+      }
+      return __builtin_amdgcn_readlane(pgv, uniform((tok >> pshift) - pwin));
+    };
 
     float m = kNegInf;
     float lsum = 0.f;
-    float acc[NC][8];
+    f32x4 o[8];
 #pragma unroll
-    for (int n = 0; n < NC; ++n)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[n][e] = 0.f;
+    for (int db = 0; db < 8; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const size_t row_elems = (size_t)a.hkv * kHeadDim;
-    const uint16_t* kbase = a.kc + (size_t)kvh * kHeadDim;
-    const uint16_t* vbase = a.vc + (size_t)kvh * kHeadDim;
-
-    for (int t = t0; t < t1; t += 16 * NB) {
-      u32x4 kf[NB][4];
-      u32x4 vf[NB][4];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int tok = t + 16 * b;
-        if (tok < t1) {
-          const int pg = uniform(a.pages[s.page_off + (tok >> pshift)]);
-          const size_t slot0 = ((size_t)pg << pshift) + (size_t)(tok & pmask);
-          const uint16_t* kp = kbase + (slot0 + L) * row_elems + 8 * J;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) kf[b][k] = ld16(kp + 32 * k);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint16_t* vp = vbase + (slot0 + 4 * J + r) * row_elems + 8 * L;
-            u32x4 v = ld16(vp);
-            // Tokens past the item end hold stale cache contents; zero them so
-            // that 0 * (stale) can never become NaN.
-            if (tok + 4 * J + r >= t1) v = u32x4{0u, 0u, 0u, 0u};
-            vf[b][r] = v;
-          }
-        } else {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            kf[b][k] = u32x4{0u, 0u, 0u, 0u};
-            vf[b][k] = u32x4{0u, 0u, 0u, 0u};
-          }
-        }
+    int stage = 0;
+    for (int tok = t0; tok < t1; tok += 16) {
+      const bool more = tok + 16 < t1;
+      if (more) {
+        const int pg = page_of(tok + 16);
+        wait_lds();
+        issue(tok + 16, pg, stage ^ 1);
+        wait_vmem<8>();
+      } else {
+        wait_vmem<0>();
       }
+      const uint32_t st = ring + (uint32_t)(stage * kDecStage);
 
-      // S^T = K Q^T, 16 tokens x 16 columns per block.
-      float x[NB][4];
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sc = mfma16<BF16>(lds_read16(st + k_lds[k]), qf[k], sc);
+
+      float x[4];
       float mx = kNegInf;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) sc = mfma16<BF16>(kf[b][k], qf[k], sc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = t + 16 * b + 4 * J + r;
-          const float v = tok <= lim ? sc[r] * a.scale_log2 : kNegInf;
-          x[b][r] = v;
-          mx = fmaxf(mx, v);
-        }
+      for (int r = 0; r < 4; ++r) {
+        x[r] = tok + 4 * J + r <= lim ? sc[r] * a.scale_log2 : kNegInf;
+        mx = fmaxf(mx, x[r]);
       }
       mx = fmaxf(mx, xor16(mx));
       mx = fmaxf(mx, xor32(mx));
@@ -147,77 +263,58 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a, int causal
       const float alpha = fast_exp2(m - m_use);
       float ps = 0.f;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[b][r] = fast_exp2(x[b][r] - m_use);
-          ps += x[b][r];
-        }
+      for (int r = 0; r < 4; ++r) {
+        x[r] = fast_exp2(x[r] - m_use);
+        ps += x[r];
+      }
       lsum = lsum * alpha + ps;
       m = m_new;
+      const u32x2 pf = {pack2<BF16>(x[0], x[1]), pack2<BF16>(x[2], x[3])};
 
-      static_for<0, NC>([&](auto n) {
-        const float an = row_bcast<n>(alpha);
+      if (!more && t1 - tok < 16) {
+        // Rows past the item end hold stale cache contents: zero them so that
+        // 0 * (stale) can never become NaN.  (16-byte slot q holds part of
+        // token row q / 16.)
+        typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[n][e] *= an;
-      });
-
-      // O += P V on the VALU: lane group J owns tokens 4*J + r of each block.
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v[8];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[2 * i] = lo_f32<BF16>(vf[b][r][i]);
-            v[2 * i + 1] = hi_f32<BF16>(vf[b][r][i]);
-          }
-          const float pv = x[b][r];
-          static_for<0, NC>([&](auto n) {
-            const float pn = row_bcast<n>(pv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[n][e] += pn * v[e];
-          });
+        for (int u = 0; u < 4; ++u) {
+          const int q = lane + 64 * u;
+          if ((q >> 4) >= t1 - tok) *(lds_u32x4*)(uintptr_t)(st + 4096 + 16 * q) = u32x4{0u, 0u, 0u, 0u};
         }
+      }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db] *= alpha;
+      }
+      u32x2 vf[8];
+#pragma unroll
+      for (int db = 0; db < 8; ++db) vf[db] = lds_read_tr16(st + v_lds[db]);
+#pragma unroll
+      for (int db = 0; db < 8; ++db) o[db] = mfma16k16<BF16>(vf[db], pf, o[db]);
+      stage ^= 1;
     }
 
-    // Combine the four lane groups (disjoint token subsets).
     lsum += xor16(lsum);
     lsum += xor32(lsum);
+    if (col_ok) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const float l2 = lsum > 0.f ? m + __log2f(lsum) : kNegInf;
+      if (w.part < 0) {
+        uint16_t* op = a.out + ((size_t)crow * a.hq + chead) * kHeadDim + 4 * J;
 #pragma unroll
-    for (int n = 0; n < NC; ++n)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc[n][e] += xor16(acc[n][e]);
-        acc[n][e] += xor32(acc[n][e]);
-      }
-
-    static_for<0, NC>([&](auto n) {
-      const float ln = row_bcast<n>(lsum);
-      const float mn = row_bcast<n>(m);
-      if (n < ncols && J == (n & 3)) {
-        const int row = w.q0 + n / G;
-        const int head = kvh * G + n % G;
-        const float inv = ln > 0.f ? 1.f / ln : 0.f;
-        const float l2 = ln > 0.f ? mn + __log2f(ln) : kNegInf;
-        if (w.part < 0) {
-          u32x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = pack2<BF16>(acc[n][2 * i] * inv, acc[n][2 * i + 1] * inv);
-          *reinterpret_cast<u32x4*>(a.out + ((size_t)row * a.hq + head) * kHeadDim + 8 * L) = o;
-          if (a.lse != nullptr && L == 0) a.lse[(size_t)row * a.hq + head] = l2 * kLn2;
-        } else {
-          const size_t slot = (size_t)(w.part + n / G);
-          float* po = a.part_o + (slot * a.hq + head) * kHeadDim + 8 * L;
-          f32x4 o0 = {acc[n][0] * inv, acc[n][1] * inv, acc[n][2] * inv, acc[n][3] * inv};
-          f32x4 o1 = {acc[n][4] * inv, acc[n][5] * inv, acc[n][6] * inv, acc[n][7] * inv};
-          reinterpret_cast<f32x4*>(po)[0] = o0;
-          reinterpret_cast<f32x4*>(po)[1] = o1;
-          if (L == 0) a.part_lse[slot * a.hq + head] = l2;
+        for (int db = 0; db < 8; ++db) {
+          const u32x2 v = {pack2<BF16>(o[db][0] * inv, o[db][1] * inv), pack2<BF16>(o[db][2] * inv, o[db][3] * inv)};
+          *reinterpret_cast<u32x2*>(op + 16 * db) = v;
         }
+        if (a.lse != nullptr && J == 0) a.lse[(size_t)crow * a.hq + chead] = l2 * kLn2;
+      } else {
+        const size_t slot = (size_t)(w.part + L / G);
+        float* po = a.part_o + (slot * a.hq + chead) * kHeadDim + 4 * J;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db] * inv;
+        if (J == 0) a.part_lse[slot * a.hq + chead] = l2;
       }
-    });
+    }
   }
 }
 
@@ -456,60 +553,90 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
 // ===========================================================================
 // Split-KV merge
 // ===========================================================================
-// One workgroup per merged row; thread handles 4 dims of one head per pass.
+// One wavefront per (merged row, head); lane owns 2 of the 128 dims.  The
+// split log-sum-exps are loaded one per lane (nsplit <= 64 per pass) and
+// reduced with wavefront shuffles; the partial rows are then read with up to
+// eight splits in flight.
 template <bool BF16>
 __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
-  const int n_rows = uniform(*a.n_rows);
+  const int lane = threadIdx.x & 63;
   const int hq = a.hq;
-  for (int idx = blockIdx.x; idx < n_rows; idx += gridDim.x) {
-    const MergeRow mr = a.rows[idx];
-    for (int e = threadIdx.x; e < hq * 32; e += blockDim.x) {
-      const int h = e >> 5;
-      const int d = (e & 31) * 4;
-      float mx = kNegInf;
-      for (int sp = 0; sp < mr.nsplit; ++sp)
-        mx = fmaxf(mx, a.part_lse[(size_t)(mr.part + sp * mr.stride) * hq + h]);
-      const float mu = mx == kNegInf ? 0.f : mx;
-      float wsum = 0.f;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < mr.nsplit; ++sp) {
+  const int n_pairs = uniform(*a.n_rows) * hq;
+  for (int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6); pair < n_pairs; pair += gridDim.x * 4) {
+    const MergeRow mr = a.rows[pair / hq];
+    const int h = pair % hq;
+    // Online merge over batches of 8 splits; each batch's log-sum-exps and
+    // partial rows are all requested before any is used.
+    float m = kNegInf, wsum = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int sp0 = 0; sp0 < mr.nsplit; sp0 += 8) {
+      float l[8];
+      float2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sp = min(sp0 + u, mr.nsplit - 1);
         const size_t slot = (size_t)(mr.part + sp * mr.stride);
-        const float wgt = fast_exp2(a.part_lse[slot * hq + h] - mu);
-        wsum += wgt;
-        acc += wgt * *reinterpret_cast<const f32x4*>(a.part_o + (slot * hq + h) * kHeadDim + d);
+        l[u] = sp0 + u < mr.nsplit ? a.part_lse[slot * hq + h] : kNegInf;
+        v[u] = *reinterpret_cast<const float2*>(a.part_o + (slot * hq + h) * kHeadDim + 2 * lane);
       }
-      const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-      u32x2 v = {pack2<BF16>(acc[0] * inv, acc[1] * inv), pack2<BF16>(acc[2] * inv, acc[3] * inv)};
-      *reinterpret_cast<u32x2*>(a.out + ((size_t)mr.row * hq + h) * kHeadDim + d) = v;
-      if (a.lse != nullptr && d == 0)
-        a.lse[(size_t)mr.row * hq + h] = wsum > 0.f ? (mu + __log2f(wsum)) * kLn2 : kNegInf;
+      float bm = m;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) bm = fmaxf(bm, l[u]);
+      const float mu = bm == kNegInf ? 0.f : bm;
+      const float sc = fast_exp2(m - mu);
+      wsum *= sc;
+      o0 *= sc;
+      o1 *= sc;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wt = fast_exp2(l[u] - mu);
+        wsum += wt;
+        o0 += wt * v[u].x;
+        o1 += wt * v[u].y;
+      }
+      m = bm;
     }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const size_t oi = (size_t)mr.row * hq + h;
+    *reinterpret_cast<uint32_t*>(a.out + oi * kHeadDim + 2 * lane) = pack2<BF16>(o0 * inv, o1 * inv);
+    if (a.lse != nullptr && lane == 0) a.lse[oi] = wsum > 0.f ? (m + __log2f(wsum)) * kLn2 : kNegInf;
   }
 }
 
 // ===========================================================================
 // Launchers
 // ===========================================================================
-template <bool BF16>
-static hipError_t decode_dispatch(const AttnArgs& a, int nc, int causal, int grid, hipStream_t st) {
-  switch (nc) {
-    case 4:
-      hipLaunchKernelGGL((attn_decode_kernel<BF16, 4, 4>), dim3(grid), dim3(256), 0, st, a, causal);
-      break;
-    case 8:
-      hipLaunchKernelGGL((attn_decode_kernel<BF16, 8, 2>), dim3(grid), dim3(256), 0, st, a, causal);
-      break;
-    case 16:
-      hipLaunchKernelGGL((attn_decode_kernel<BF16, 16, 2>), dim3(grid), dim3(256), 0, st, a, causal);
-      break;
-    default:
-      return hipErrorInvalidValue;
+#ifndef FEATTN_DECODE_WAVES
+#define FEATTN_DECODE_WAVES 8
+#endif
+constexpr int kDecodeWaves = FEATTN_DECODE_WAVES;
+
+int decode_waves() { return kDecodeWaves; }
+
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st) {
+  (void)nc;  // one MFMA column block serves every decode item (<= 16 columns)
+  const size_t lds = (size_t)kDecodeWaves * kDecStages * kDecStage;
+  static bool lds_ok[2] = {false, false};  // the ring exceeds the 64 KB default
+  if (!lds_ok[bf16]) {
+    hipError_t e = bf16 ? hipFuncSetAttribute((const void*)attn_decode_kernel<true, kDecodeWaves>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)
+                        : hipFuncSetAttribute((const void*)attn_decode_kernel<false, kDecodeWaves>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    lds_ok[bf16] = true;
   }
+  if (bf16)
+    hipLaunchKernelGGL((attn_decode_kernel<true, kDecodeWaves>), dim3(grid), dim3(64 * kDecodeWaves), lds, st, a,
+                       causal);
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<false, kDecodeWaves>), dim3(grid), dim3(64 * kDecodeWaves), lds, st, a,
+                       causal);
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st) {
-  return bf16 ? decode_dispatch<true>(a, nc, causal, grid, st) : decode_dispatch<false>(a, nc, causal, grid, st);
+hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st) {
+  if (bf16) hipLaunchKernelGGL((attn_merge_kernel<true>), dim3(grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((attn_merge_kernel<false>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st) {
@@ -520,12 +647,6 @@ hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipS
     if (causal) hipLaunchKernelGGL((attn_tile_kernel<false, true>), dim3(grid), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((attn_tile_kernel<false, false>), dim3(grid), dim3(256), 0, st, a);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st) {
-  if (bf16) hipLaunchKernelGGL((attn_merge_kernel<true>), dim3(grid), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((attn_merge_kernel<false>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

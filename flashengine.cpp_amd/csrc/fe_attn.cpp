@@ -21,6 +21,7 @@
 
 namespace feattn {
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st);
+int decode_waves();
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
@@ -140,9 +141,9 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   p->bf16 = bf16 != 0;
   p->device = dev;
   p->lay = make_layout(sh);
-  p->grid_decode_cap = sh.num_cus * 2;  // 4 waves per workgroup, 8 resident waves per CU
+  p->grid_decode_cap = sh.num_cus * 16 / decode_waves();  // 16 wavefronts per CU
   p->grid_tile_cap = sh.num_cus * 2;    // 2 resident 256-thread tile workgroups per CU
-  p->grid_merge_cap = sh.num_cus * 4;
+  p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head) pairs per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
     fe_attn_plan_destroy(p);
     return fail(code, msg);
@@ -158,8 +159,8 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (hipEventCreateWithFlags(&p->staged, hipEventDisableTiming) != hipSuccess)
     return cleanup(FE_EDEVICE, "hipEventCreate failed");
   // Counts start at zero so a run before any prepare does nothing.
-  if (hipMemset(p->dev + p->lay.counts, 0, sizeof(int32_t) * 8) != hipSuccess)
-    return cleanup(FE_EDEVICE, "hipMemset(counts) failed");
+  if (hipMemset(p->dev, 0, p->lay.total) != hipSuccess) return cleanup(FE_EDEVICE, "hipMemset(plan) failed");
+  if (hipDeviceSynchronize() != hipSuccess) return cleanup(FE_EDEVICE, "hipDeviceSynchronize failed");
   *plan_out = p;
   return FE_OK;
 }
@@ -275,7 +276,8 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     AttnArgs d = a;
     d.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.decode);
     d.n_items = counts + kCntDecode;
-    const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + 3) / 4);
+    const int wv = decode_waves();
+    const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + wv - 1) / wv);
     e = launch_decode(d, p->bf16, p->decode_nc, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
@@ -296,7 +298,8 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     m.part_o = p->part_o;
     m.part_lse = p->part_lse;
     m.hq = p->sh.hq;
-    const int grid = p->graph ? p->grid_merge_cap : std::min(p->grid_merge_cap, p->n_merge[mode]);
+    const int pairs4 = (int)(((int64_t)p->n_merge[mode] * p->sh.hq + 3) / 4);
+    const int grid = p->graph ? p->grid_merge_cap : std::min(p->grid_merge_cap, pairs4);
     e = launch_merge(m, p->bf16, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
   }

@@ -11,6 +11,11 @@ namespace feattn {
 
 namespace {
 
+#ifndef FEATTN_DECODE_ITEMS_PER_CU
+#define FEATTN_DECODE_ITEMS_PER_CU 16
+#endif
+constexpr int kDecodeItemsPerCu = FEATTN_DECODE_ITEMS_PER_CU;
+
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
@@ -131,7 +136,7 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
     // About 16 work items per compute unit (4 resident waves each, several
     // rounds) with at least 128 tokens per item; splits cost one fp32 partial
     // row per query row, so the chunk grows until the partials fit.
-    const int64_t target = (int64_t)sh.num_cus * 16;
+    const int64_t target = (int64_t)sh.num_cus * kDecodeItemsPerCu;
     int chunk = (int)std::min<int64_t>(1 << 20, (decode_tokens + target - 1) / target);
     chunk = std::max(128, round_up(chunk, 64));
     for (;;) {

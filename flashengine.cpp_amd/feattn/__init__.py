@@ -18,7 +18,7 @@ import os
 from typing import Optional, Sequence
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libfeattn.so")
+LIB_PATH = os.environ.get("FEATTN_LIB") or os.path.join(PKG_DIR, "lib", "libfeattn.so")
 
 FE_OK = 0
 FE_EINVAL = -1
