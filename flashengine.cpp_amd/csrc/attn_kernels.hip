@@ -57,17 +57,22 @@ __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
 // ===========================================================================
 // Decode kernel
 // ===========================================================================
-// One wavefront per work item of <= 16 (query row, head) columns; WAVES
-// wavefronts per workgroup take consecutive items, which the planner orders
-// (sequence, chunk, kv head), so a workgroup streams whole pages of the cache.
+// Each wavefront slot owns one kv head and one share of the decode token
+// stream (the planner's equal cut of all decode sequences, each piece a
+// sequence's work item of <= 16 (query row, head) columns).  Consecutive
+// slots are consecutive kv heads of the same share, so the WAVES wavefronts
+// of a workgroup stream the same cache pages together.
 //
-// K and V of each 16-token block are copied HBM -> LDS by direct-to-LDS loads
-// (global_load_lds_dwordx4: lane i of an instruction lands at LDS base + 16 i)
-// into a two-stage ring private to the wavefront; the next block's copy is in
-// flight while the current one is computed.  Every copy instruction moves
-// four whole 256-byte token rows.  Inside a stage, the 16-byte chunk c of
-// token row t is stored at chunk position c ^ t (K) or c ^ (2t mod 16) (V),
-// which makes both operand reads below free of LDS bank conflicts.
+// HBM -> LDS copies use direct-to-LDS loads (global_load_lds_dwordx4: lane i
+// of an instruction lands at LDS base + 16 i).  Each wavefront owns a
+// two-stage ring (one 16-token block of K then V per stage) and a Q buffer.
+// The copy of the next block -- at an item's last block, the next item's Q
+// and first block -- is in flight while the current block is computed, so
+// item boundaries do not drain the pipeline.  Every copy instruction moves
+// four whole 256-byte rows; inside a stage, 16-byte chunk c of row t sits at
+// chunk position c ^ t (K, Q) or c ^ (2t mod 16) (V), which makes the operand
+// reads below free of LDS bank conflicts.  Page ids are read with scalar
+// loads one block ahead of their use.
 //
 // Lane = 16*J + L.  Per block:
 //   S^T = K Q^T:  A = K rows (lane: token L, dims 32s+8J..+8, ds_read_b128),
@@ -78,8 +83,9 @@ __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
 //                 4J..4J+3 = its own S^T values), 8 x 16x16x16 MFMA;
 //                 C: lane holds dims 16db+4J+r of column L.
 // Softmax statistics are per column, i.e. per lane (reduced over J).
-constexpr int kDecStage = 8192;    // LDS bytes per 16-token block (K then V)
-constexpr int kDecStages = 2;
+constexpr int kDecStage = 8192;                        // one 16-token block: K (4 KB) then V (4 KB)
+constexpr int kDecQ = 4096;                            // Q of one item: 16 columns x 256 bytes
+constexpr int kDecWaveLds = 2 * kDecStage + kDecQ;     // per wavefront
 
 __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
   uint32_t saved;
@@ -125,6 +131,11 @@ __device__ __forceinline__ u32x4 lds_read16(uint32_t lds_addr) {
   return *(lds_u32x4*)(uintptr_t)lds_addr;
 }
 
+__device__ __forceinline__ void lds_zero16(uint32_t lds_addr) {
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  *(lds_u32x4*)(uintptr_t)lds_addr = u32x4{0u, 0u, 0u, 0u};
+}
+
 template <bool BF16, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int causal) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
@@ -136,20 +147,20 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
   const int G = a.group;
   const int pshift = a.page_shift;
   const int pmask = (1 << pshift) - 1;
-  const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * kDecStages * kDecStage);
+  const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * kDecWaveLds);
+  const uint32_t qbuf = ring + 2 * kDecStage;
 
   // Per-lane pieces of the copy and read addresses (fixed for the kernel).
-  // Copy instruction r, lane i = 16*J + L: token row 4r + J, chunk position L;
-  // the global chunk is L ^ row (K) or L ^ (2 row mod 16) (V).
-  int k_goff[4], v_goff[4];
+  // Copy instruction r, lane i = 16*J + L: row 4r + J, chunk position L.
   const int row_bytes = a.hkv * kHeadDim * 2;
+  int k_goff[4], v_goff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = 4 * r + J;
     k_goff[r] = t * row_bytes + 16 * (L ^ t);
     v_goff[r] = t * row_bytes + 16 * (L ^ ((2 * t) & 15));
   }
-  // K operand chunk position for k-step s: token L, chunk (4s + J) ^ L.
+  // K operand for k-step s: token L, chunk 4s + J; Q operand: column L, same chunk.
   uint32_t k_lds[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) k_lds[s] = (uint32_t)(16 * (16 * L + (((4 * s + J) ^ L) & 15)));
@@ -165,14 +176,61 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
     }
   }
 
-  for (int it = blockIdx.x * WAVES + wave; it < n_items; it += gridDim.x * WAVES) {
-    const WorkItem w = ldc_item(a.items, it);
-    const SeqInfo s = ldc_seq(a.seqs, w.seq);
-    const int kvh = w.kvh;
+  // Wavefront slot -> (kv head, share): consecutive slots are consecutive
+  // kv heads of one share.  n_items counts the shares in use.
+  const int slot = blockIdx.x * WAVES + wave;
+  if (slot >= n_items * a.hkv) return;
+  const int kvh = slot % a.hkv;
+  const int share = slot / a.hkv;
+  int it = ldc(a.share_off, share);
+  const int it_end = ldc(a.share_off, share + 1);
+  if (it >= it_end) return;
+
+  auto page_id = [&](const SeqInfo& sq, int tok) { return ldc(a.pages, sq.page_off + (tok >> pshift)); };
+  // Copies one 16-token block of this wavefront's kv head into ring stage `stage`.
+  auto copy_block = [&](int tok, int pg, int stage) {
+    const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
+    const char* kb = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2 + blk;
+    const char* vb = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2 + blk;
+    const uint32_t st = ring + (uint32_t)(stage * kDecStage);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lds_dma16(kb + k_goff[r], st + 1024 * r);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lds_dma16(vb + v_goff[r], st + 4096 + 1024 * r);
+  };
+  // Copies the 16 Q^T columns of an item (columns past nq*G repeat column 0).
+  auto copy_q = [&](const WorkItem& wi) {
+    const int nc = wi.nq * G;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = 4 * r + J;
+      const int nn = n < nc ? n : 0;
+      const int row = wi.q0 + nn / G;
+      const int head = kvh * G + nn % G;
+      lds_dma16(a.q + ((size_t)row * a.hq + head) * kHeadDim + 8 * (L ^ n), qbuf + 1024 * r);
+    }
+  };
+
+  WorkItem w = ldc_item(a.items, it);
+  SeqInfo s = ldc_seq(a.seqs, w.seq);
+  copy_q(w);
+  copy_block(w.t0, page_id(s, w.t0), 0);
+  int stage = 0;
+  // Page id of the block the next copy will fetch; -1 = not yet read.
+  int pg_next = w.t0 + 16 < w.t1 ? page_id(s, w.t0 + 16) : -1;
+
+  for (;;) {
+    const int nit = it + 1;
+    const bool has_next = nit < it_end;
+    WorkItem wn = w;
+    SeqInfo sn = s;
+    if (has_next) {
+      wn = ldc_item(a.items, nit);
+      sn = ldc_seq(a.seqs, wn.seq);
+    }
     const int t0 = w.t0;
     const int t1 = w.t1;
     const int ncols = w.nq * G;
-
     const bool col_ok = L < ncols;
     const int crow = w.q0 + (col_ok ? L / G : 0);
     const int chead = kvh * G + (col_ok ? L % G : 0);
@@ -182,49 +240,15 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       lim = min(lim, t1 - 1);
     }
 
-    const char* kbase = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
-    const char* vbase = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
-    auto issue = [&](int tok, int pg, int stage) {
-      const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
-      const uint32_t st = ring + (uint32_t)(stage * kDecStage);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(kbase + blk + k_goff[r], st + 1024 * r);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(vbase + blk + v_goff[r], st + 4096 + 1024 * r);
-    };
-
-    // Item start: the first block's copy (its page id by a scalar load), the
-    // item's page ids (one per lane, in windows of 64 pages) and the Q^T
-    // operand (column L) are all in flight before the one wait for them.  The empty asm then hands the registers on as plain
-    // values, so no wait for them lands inside the token loop, where the
-    // next block's copy is in flight.
-    wait_lds();  // earlier reads of the ring are complete before it is refilled
-    issue(t0, ldc(a.pages, s.page_off + (t0 >> pshift)), 0);
-    const int plast = (t1 - 1) >> pshift;
-    int pwin = t0 >> pshift;
-    auto window = [&](int first) {
-      const int idx = first + lane;
-      return idx <= plast ? a.pages[s.page_off + idx] : 0;
-    };
-    int pgv = window(pwin);
+    // This item's Q was copied before its first block: at most the 8 block
+    // copies (and younger stores) may still be outstanding.
+    wait_vmem<8>();
     u32x4 qf[4];
-    {
-      const uint16_t* qp = a.q + ((size_t)crow * a.hq + chead) * kHeadDim + 8 * J;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) qf[k] = ld16(qp + 32 * k);
-      asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(pgv));
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
+    for (int k = 0; k < 4; ++k) {
+      qf[k] = lds_read16(qbuf + k_lds[k]);
+      if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
     }
-    auto page_of = [&](int tok) {
-      if ((tok >> pshift) - pwin >= 64) {  // next window (long items only)
-        pwin += 64;
-        pgv = window(pwin);
-        asm volatile("" : "+v"(pgv));
-      }
-      return __builtin_amdgcn_readlane(pgv, uniform((tok >> pshift) - pwin));
-    };
 
     float m = kNegInf;
     float lsum = 0.f;
@@ -232,14 +256,21 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    int stage = 0;
     for (int tok = t0; tok < t1; tok += 16) {
       const bool more = tok + 16 < t1;
       if (more) {
-        const int pg = page_of(tok + 16);
-        wait_lds();
-        issue(tok + 16, pg, stage ^ 1);
+        const int pg = pg_next >= 0 ? pg_next : page_id(s, tok + 16);
+        wait_lds();  // the stage being refilled was last read one block ago
+        copy_block(tok + 16, pg, stage ^ 1);
+        pg_next = tok + 32 < t1 ? page_id(s, tok + 32) : (has_next ? page_id(sn, wn.t0) : -1);
         wait_vmem<8>();
+      } else if (has_next) {
+        const int pg = pg_next >= 0 ? pg_next : page_id(sn, wn.t0);
+        wait_lds();  // also: this item's Q has been read
+        copy_q(wn);
+        copy_block(wn.t0, pg, stage ^ 1);
+        pg_next = wn.t0 + 16 < wn.t1 ? page_id(sn, wn.t0 + 16) : -1;
+        wait_vmem<12>();
       } else {
         wait_vmem<0>();
       }
@@ -275,11 +306,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
         // Rows past the item end hold stale cache contents: zero them so that
         // 0 * (stale) can never become NaN.  (16-byte slot q holds part of
         // token row q / 16.)
-        typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int q = lane + 64 * u;
-          if ((q >> 4) >= t1 - tok) *(lds_u32x4*)(uintptr_t)(st + 4096 + 16 * q) = u32x4{0u, 0u, 0u, 0u};
+          if ((q >> 4) >= t1 - tok) lds_zero16(st + 4096 + 16 * q);
         }
       }
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
@@ -315,6 +345,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
         if (J == 0) a.part_lse[slot * a.hq + chead] = l2;
       }
     }
+    if (!has_next) break;
+    it = nit;
+    w = wn;
+    s = sn;
   }
 }
 
@@ -612,9 +646,12 @@ constexpr int kDecodeWaves = FEATTN_DECODE_WAVES;
 
 int decode_waves() { return kDecodeWaves; }
 
+// Workgroups of the decode kernel that fit one CU at once (160 KB of LDS).
+int decode_wgs_per_cu() { return (int)(163840 / ((size_t)kDecodeWaves * kDecWaveLds)); }
+
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st) {
   (void)nc;  // one MFMA column block serves every decode item (<= 16 columns)
-  const size_t lds = (size_t)kDecodeWaves * kDecStages * kDecStage;
+  const size_t lds = (size_t)kDecodeWaves * kDecWaveLds;
   static bool lds_ok[2] = {false, false};  // the ring exceeds the 64 KB default
   if (!lds_ok[bf16]) {
     hipError_t e = bf16 ? hipFuncSetAttribute((const void*)attn_decode_kernel<true, kDecodeWaves>,

@@ -59,6 +59,7 @@ struct AttnArgs {
   const int32_t* pages;
   const WorkItem* items;
   const int32_t* n_items;  // device-resident count (graph replays read the current one)
+  const int32_t* share_off;  // decode only: pieces of share k = items[share_off[k] .. share_off[k+1])
   float* part_o;           // [slots][hq][128] fp32, normalised per split
   float* part_lse;         // [slots][hq] log2 domain
   int hq;

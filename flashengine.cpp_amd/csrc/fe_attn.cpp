@@ -22,6 +22,7 @@
 namespace feattn {
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st);
 int decode_waves();
+int decode_wgs_per_cu();
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
@@ -52,7 +53,7 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Offsets of the regions inside the metadata arena (same layout on host and device).
 struct Layout {
-  size_t seqs, pages, counts, decode, tile[2], merge[2], total;
+  size_t seqs, pages, counts, dshare, decode, tile[2], merge[2], total;
 };
 
 Layout make_layout(const PlanShape& sh) {
@@ -64,6 +65,8 @@ Layout make_layout(const PlanShape& sh) {
   off = align256(off + sizeof(int32_t) * (size_t)sh.max_batch * sh.max_pages);
   l.counts = off;
   off = align256(off + sizeof(int32_t) * 8);
+  l.dshare = off;
+  off = align256(off + sizeof(int32_t) * ((size_t)sh.decode_waves + 2));
   l.decode = off;
   off = align256(off + sizeof(WorkItem) * sh.item_cap);
   for (int m = 0; m < 2; ++m) {
@@ -136,12 +139,13 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
   sh.num_cus = cus > 0 ? cus : 256;
 
+  sh.decode_waves = sh.num_cus * decode_wgs_per_cu() * decode_waves();
   auto* p = new fe_attn_plan();
   p->sh = sh;
   p->bf16 = bf16 != 0;
   p->device = dev;
   p->lay = make_layout(sh);
-  p->grid_decode_cap = sh.num_cus * 16 / decode_waves();  // 16 wavefronts per CU
+  p->grid_decode_cap = sh.num_cus * decode_wgs_per_cu();  // persistent: every workgroup resident
   p->grid_tile_cap = sh.num_cus * 2;    // 2 resident 256-thread tile workgroups per CU
   p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head) pairs per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
@@ -207,7 +211,9 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
   if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
   int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
-  cnt[kCntDecode] = (int32_t)bp.decode.size();
+  const int n_shares = bp.decode_share_off.empty() ? 0 : (int)bp.decode_share_off.size() - 1;
+  cnt[kCntDecode] = n_shares;
+  std::memcpy(h + l.dshare, bp.decode_share_off.data(), sizeof(int32_t) * bp.decode_share_off.size());
   cnt[kCntTile0] = (int32_t)bp.mode[0].tile.size();
   cnt[kCntTile1] = (int32_t)bp.mode[1].tile.size();
   cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
@@ -225,6 +231,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e == hipSuccess) e = copy(l.seqs, sizeof(SeqInfo) * bp.seqs.size());
   if (e == hipSuccess) e = copy(l.pages, sizeof(int32_t) * npages);
   if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
+  if (e == hipSuccess) e = copy(l.dshare, sizeof(int32_t) * bp.decode_share_off.size());
   if (e == hipSuccess) e = copy(l.decode, sizeof(WorkItem) * bp.decode.size());
   for (int m = 0; m < 2 && e == hipSuccess; ++m) {
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
@@ -237,7 +244,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   p->prepared = true;
   p->graph = graph != 0;
   p->decode_nc = nc;
-  p->n_decode = (int)bp.decode.size();
+  p->n_decode = n_shares * p->sh.hkv;  // busy decode wavefronts
   for (int m = 0; m < 2; ++m) {
     p->n_tile[m] = (int)bp.mode[m].tile.size();
     p->n_merge[m] = (int)bp.mode[m].merge.size();
@@ -275,6 +282,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
   if (p->graph || p->n_decode > 0) {
     AttnArgs d = a;
     d.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.decode);
+    d.share_off = reinterpret_cast<const int32_t*>(p->dev + p->lay.dshare);
     d.n_items = counts + kCntDecode;
     const int wv = decode_waves();
     const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + wv - 1) / wv);
@@ -362,7 +370,7 @@ int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int
   const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   if (counts_out) {
-    counts_out[0] = (int32_t)bp.decode.size();
+    counts_out[0] = (int32_t)bp.decode.size() * hkv;
     counts_out[1] = (int32_t)bp.mode[1].tile.size();
     counts_out[2] = (int32_t)bp.mode[1].merge.size();
     counts_out[3] = bp.mode[1].partial_rows;
@@ -401,7 +409,13 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch, int max
     }
     ++n;
   };
-  for (const WorkItem& w : bp.decode) emit(0, w);
+  for (size_t k = 0; k + 1 < bp.decode_share_off.size(); ++k)
+    for (int h = 0; h < hkv; ++h)
+      for (int i = bp.decode_share_off[k]; i < bp.decode_share_off[k + 1]; ++i) {
+        WorkItem w = bp.decode[i];
+        w.kvh = h;
+        emit(0, w);
+      }
   for (const WorkItem& w : bp.mode[causal ? 1 : 0].tile) emit(1, w);
   if (n_out) *n_out = n;
   return FE_OK;

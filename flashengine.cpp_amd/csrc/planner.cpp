@@ -11,10 +11,9 @@ namespace feattn {
 
 namespace {
 
-#ifndef FEATTN_DECODE_ITEMS_PER_CU
-#define FEATTN_DECODE_ITEMS_PER_CU 16
-#endif
-constexpr int kDecodeItemsPerCu = FEATTN_DECODE_ITEMS_PER_CU;
+// Shortest decode share: below this, per-piece start-up and merge cost more
+// than the extra wavefronts gain.
+constexpr int64_t kMinShareTokens = 64;
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
@@ -121,59 +120,73 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
   const int G = sh.hq / sh.hkv;
   const int slot_budget = sh.partial_cap;
 
-  // ---- decode items: sequences whose (rows x group) fit one MFMA column block.
-  int64_t decode_tokens = 0;
+  // ---- decode pieces: sequences whose (rows x group) fit one MFMA column
+  // block.  Each kv head's token stream -- the decode sequences one after
+  // another, each padded to whole 16-token blocks -- is cut into equal
+  // shares, one per decode wavefront slot (decode_waves / hkv shares); a
+  // share's pieces are its intersections with the sequences.  Every kv head
+  // uses the same cut, so the wavefronts of one workgroup (consecutive kv
+  // heads of one share) read the same pages at the same time.  A sequence
+  // cut into several pieces is merged by log-sum-exp afterwards; when the
+  // partials would not fit, shares grow (fewer wavefronts busy).
   int max_cols = 0;
+  int64_t stream = 0;
   for (int b = 0; b < batch; ++b) {
     const SeqInfo& s = out.seqs[b];
     if (s.qlen > 0 && s.qlen * G <= kDecodeCols) {
-      decode_tokens += (int64_t)s.len * sh.hkv;
+      stream += round_up(s.len, 16);
       max_cols = std::max(max_cols, s.qlen * G);
     }
   }
   out.decode_nc = max_cols <= 4 ? 4 : max_cols <= 8 ? 8 : 16;
-  if (decode_tokens > 0) {
-    // About 16 work items per compute unit (4 resident waves each, several
-    // rounds) with at least 128 tokens per item; splits cost one fp32 partial
-    // row per query row, so the chunk grows until the partials fit.
-    const int64_t target = (int64_t)sh.num_cus * kDecodeItemsPerCu;
-    int chunk = (int)std::min<int64_t>(1 << 20, (decode_tokens + target - 1) / target);
-    chunk = std::max(128, round_up(chunk, 64));
+  const int shares = std::max(1, sh.decode_waves / sh.hkv);
+  if (stream > 0) {
+    int64_t quota = std::max<int64_t>(kMinShareTokens, round_up((int)((stream + shares - 1) / shares), 16));
     for (;;) {
-      int slots = 0;
-      size_t n_items = 0;
+      // partial slots needed with this quota
+      int64_t slots = 0, pieces = 0, off = 0;
       for (int b = 0; b < batch; ++b) {
         const SeqInfo& s = out.seqs[b];
         if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
-        const int ns = ceil_div(s.len, chunk);
-        if (ns > 1) slots += ns * s.qlen;
-        n_items += (size_t)ns * sh.hkv;
+        const int64_t end = off + round_up(s.len, 16);
+        const int64_t np = (end - 1) / quota - off / quota + 1;
+        if (np > 1) slots += np * s.qlen;
+        pieces += np;
+        off = end;
       }
-      if (slots <= slot_budget && n_items <= (size_t)sh.item_cap) break;
-      if (chunk >= (1 << 22)) {
+      if (slots <= slot_budget && pieces <= sh.item_cap) break;
+      if (quota >= stream) {
         err = "attention metadata exceeds capacity: decode work list";
         return FE_ECAPACITY;
       }
-      chunk *= 2;
+      quota *= 2;
     }
+    const int used = (int)((stream + quota - 1) / quota);
+    out.decode_share_off.assign(used + 1, 0);
+    int64_t off = 0;
+    int share = 0;
     for (int b = 0; b < batch; ++b) {
       const SeqInfo& s = out.seqs[b];
       if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
-      const int ns = ceil_div(s.len, chunk);
+      const int64_t end = off + round_up(s.len, 16);
+      const int k0 = (int)(off / quota), k1 = (int)((end - 1) / quota);
+      const int np = k1 - k0 + 1;
       int base = -1;
-      if (ns > 1) {
+      if (np > 1) {
         base = out.decode_partials;
-        out.decode_partials += ns * s.qlen;
-        for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, ns, s.qlen});
+        out.decode_partials += np * s.qlen;
+        for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, np, s.qlen});
       }
-      for (int sp = 0; sp < ns; ++sp) {
-        const int t0 = sp * chunk;
-        const int t1 = std::min<int>(s.len, t0 + chunk);
-        for (int h = 0; h < sh.hkv; ++h)
-          out.decode.push_back(WorkItem{b, s.qo, s.qlen, h, t0, t1, base < 0 ? -1 : base + sp * s.qlen, t1 - t0});
+      for (int k = k0; k <= k1; ++k) {
+        while (share < k) out.decode_share_off[++share] = (int32_t)out.decode.size();
+        const int t0 = (int)(std::max<int64_t>(off, (int64_t)k * quota) - off);
+        const int t1 = (int)std::min<int64_t>(s.len, std::min<int64_t>(end, (int64_t)(k + 1) * quota) - off);
+        out.decode.push_back(
+            WorkItem{b, s.qo, s.qlen, 0, t0, t1, base < 0 ? -1 : base + (k - k0) * s.qlen, t1 - t0});
       }
+      off = end;
     }
-    order_items(out.decode);
+    while (share < used) out.decode_share_off[++share] = (int32_t)out.decode.size();
   }
 
   // ---- tile items, per mask mode.

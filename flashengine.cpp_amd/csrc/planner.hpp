@@ -20,6 +20,7 @@ struct PlanShape {
   int max_pages = 0;
   int blocks = 0;
   int num_cus = 256;        // compute units on the device (sizes split-KV)
+  int decode_waves = 2048;  // wavefront slots of one decode launch
   int item_cap = 1 << 16;   // work items per list
   int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
 };
@@ -32,7 +33,8 @@ struct ModeLists {
 
 struct BuiltPlan {
   std::vector<SeqInfo> seqs;
-  std::vector<WorkItem> decode;  // identical for both masks (end-aligned causal)
+  std::vector<WorkItem> decode;  // decode pieces (kvh unset), identical for both masks
+  std::vector<int32_t> decode_share_off;  // CSR: pieces of share k = [off[k], off[k+1])
   int decode_partials = 0;
   std::vector<MergeRow> decode_merge;
   int decode_nc = 4;             // 4, 8 or 16 columns per decode item
