@@ -355,23 +355,28 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 // ===========================================================================
 // Tile kernel (MFMA for both products)
 // ===========================================================================
-// LDS: K tile [64 tokens][128 dims] with rows padded to 272 bytes and a
-// transposed V tile [128 dims][64 tokens] with rows padded to 136 bytes, so
-// the 16 rows read by one MFMA operand fetch fall in distinct banks.
-constexpr int kKStride = 272;
-constexpr int kVStride = 136;
-constexpr int kLdsK = kTileTokens * kKStride;
-constexpr int kLdsV = kHeadDim * kVStride;
+// Four wavefronts share 64-token K and V tiles in LDS (two-stage ring of
+// 32 KB stages: K blocks then V blocks, 16 tokens x 256 bytes each, chunk
+// swizzles as in the decode kernel).  Wavefront w copies block w of each
+// tile with direct-to-LDS loads; after its own copy lands and a barrier,
+// the next tile's copy is issued and the current tile is computed.
+//
+// Columns: an item of <= 64 (query row, head) columns gives each wavefront
+// one 16-column block, a larger item (<= 128) two.  Per wavefront and tile:
+//   S^T = K Q^T: A = K rows from LDS (lane: token 16tb+L, dims 32s+8J..+8),
+//                B = Q^T in registers; C: lane holds tokens 16tb+4J+r of
+//                column L.
+//   O^T += V^T P^T with 16x16x32 MFMA over 32-token k-steps: the P^T operand
+//                element e of lane (J, L) is token 32ks+4J+e (e < 4) or
+//                32ks+16+4J+(e-4) (e >= 4) -- the lane's own S^T values of
+//                blocks 2ks, 2ks+1 -- and the V^T operand reads the same
+//                token order with one ds_read_b64_tr_b16 per block.
+constexpr int kTileBlock = 4096;               // 16 tokens x 256 bytes
+constexpr int kTileStage = 8 * kTileBlock;     // K blocks 0..3, then V blocks 0..3
 
-// Per wavefront: columns 32*wave + 16*cb + L (cb = 0, 1).
-// S^T block (tb, cb): lane holds tokens 16*tb + 4*J + r of its column.
-// P^T operand for k-step ks covers tokens 32*ks .. 32*ks+31; lane element e
-// is token 32*ks + 4*J + e (e < 4) or 32*ks + 16 + 4*J + (e-4) (e >= 4), which
-// is exactly what the lane holds of S^T blocks 2*ks and 2*ks+1.  The V^T
-// operand reads the same token order from LDS.
 template <bool BF16, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsK + kLdsV];
+  extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -381,33 +386,85 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
   const int G = a.group;
   const int pshift = a.page_shift;
   const int pmask = (1 << pshift) - 1;
-  const size_t row_elems = (size_t)a.hkv * kHeadDim;
+  const int row_bytes = a.hkv * kHeadDim * 2;
+  const uint32_t lbase = (uint32_t)(uintptr_t)dsm;
+
+  int k_goff[4], v_goff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 4 * r + J;
+    k_goff[r] = t * row_bytes + 16 * (L ^ t);
+    v_goff[r] = t * row_bytes + 16 * (L ^ ((2 * t) & 15));
+  }
+  uint32_t k_lds[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) k_lds[s] = (uint32_t)(16 * (16 * L + (((4 * s + J) ^ L) & 15)));
+  uint32_t v_lds[8];
+  {
+    const int k = L >> 2, m = L & 3, t = 4 * J + k;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int c = 2 * db + (m >> 1);
+      v_lds[db] = (uint32_t)(16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
+    }
+  }
 
   for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const WorkItem w = a.items[it];
-    const SeqInfo s = a.seqs[uniform(w.seq)];
-    const int kvh = uniform(w.kvh);
-    const int t0 = uniform(w.t0);
-    const int t1 = uniform(w.t1);
-    const int ncols = uniform(w.nq) * G;
-    const bool wave_on = 32 * wave < ncols;
+    const WorkItem w = ldc_item(a.items, it);
+    const SeqInfo s = ldc_seq(a.seqs, w.seq);
+    const int kvh = w.kvh;
+    const int t0 = w.t0;
+    const int t1 = w.t1;
+    const int ncols = w.nq * G;
+    const int wcols = ncols <= 64 ? 16 : 32;  // columns per wavefront
+    const int ncb = wcols / 16;
+    const bool wave_on = wave * wcols < ncols;
 
-    int lim[2];
-    int crow[2];
-    int chead[2];
+    // This wavefront's block of a tile: K and V rows [T + 16 wave, +16).
+    const char* kb0 = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
+    const char* vb0 = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
+    auto copy_block = [&](int T, int stage) {
+      const int tok = T + 16 * wave;
+      if (tok >= t1) return;
+      const int pg = ldc(a.pages, s.page_off + (tok >> pshift));
+      const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
+      const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(kb0 + blk + k_goff[r], st + wave * kTileBlock + 1024 * r);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(vb0 + blk + v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
+    };
+
+    wait_lds();
+    copy_block(t0, 0);
+
+    int lim[2], crow[2], chead[2];
     u32x4 qf[2][4];
+    int lim_min = 1 << 30;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int n = 32 * wave + 16 * cb + L;
-      const bool ok = n < ncols;
+      const int n = wave * wcols + 16 * cb + L;
+      const bool ok = cb < ncb && n < ncols;
       crow[cb] = w.q0 + (ok ? n / G : 0);
       chead[cb] = kvh * G + (ok ? n % G : 0);
       lim[cb] = -1;
       if (ok) lim[cb] = min(CAUSAL ? s.len - s.qlen + (crow[cb] - s.qo) : s.len - 1, t1 - 1);
+      if (ok) lim_min = min(lim_min, lim[cb]);
       const uint16_t* qp = a.q + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 8 * J;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) qf[cb][k] = ok ? ld16(qp + 32 * k) : u32x4{0u, 0u, 0u, 0u};
+      for (int k = 0; k < 4; ++k) qf[cb][k] = ld16(qp + 32 * k);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (!ok) qf[cb][k] = u32x4{0u, 0u, 0u, 0u};
     }
+    // Q (and the first tile's copy, issued before it) have landed once this
+    // returns; afterwards the registers are plain values, so no wait for them
+    // falls inside the tile loop while the next copy is in flight.
+    asm volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[0][2]), "+v"(qf[0][3]), "+v"(qf[1][0]),
+                 "+v"(qf[1][1]), "+v"(qf[1][2]), "+v"(qf[1][3]));
+    // Tiles ending at or before every column's limit need no mask.
+#pragma unroll
+    for (int o_ = 32; o_ >= 1; o_ >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o_, 64));
 
     float m[2] = {kNegInf, kNegInf};
     float lsum[2] = {0.f, 0.f};
@@ -417,71 +474,27 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) o[db][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Global -> register staging of one 64-token tile.
-    u32x4 kr[4];
-    u32x4 v0[2];
-    u32x4 v1[2];
-    auto gload = [&](int T) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int qd = tid + 256 * k;
-        const int tok = T + (qd >> 4);
-        const int c = qd & 15;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (tok < t1) {
-          const int pg = a.pages[s.page_off + (tok >> pshift)];
-          const size_t slot = ((size_t)pg << pshift) + (size_t)(tok & pmask);
-          val = ld16(a.kc + slot * row_elems + (size_t)kvh * kHeadDim + 8 * c);
-        }
-        kr[k] = val;
-      }
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int qd = tid + 256 * k;
-        const int tok = T + 2 * (qd >> 4);
-        const int c = qd & 15;
-        u32x4 x0 = {0u, 0u, 0u, 0u};
-        u32x4 x1 = {0u, 0u, 0u, 0u};
-        if (tok < t1) {
-          const int pg = a.pages[s.page_off + (tok >> pshift)];
-          const size_t slot = ((size_t)pg << pshift) + (size_t)(tok & pmask);
-          const uint16_t* vp = a.vc + slot * row_elems + (size_t)kvh * kHeadDim + 8 * c;
-          x0 = ld16(vp);
-          // tok is even and pages hold a multiple of 16 tokens, so tok+1 is
-          // in the same page.
-          if (tok + 1 < t1) x1 = ld16(vp + row_elems);
-        }
-        v0[k] = x0;
-        v1[k] = x1;
-      }
-    };
-
-    gload(t0);
+    int stage = 0;
     for (int T = t0; T < t1; T += kTileTokens) {
-      __syncthreads();
+      wait_vmem<0>();  // this wavefront's block of the tile has landed
+      const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
+      {
+        // rows at or past the item end: zero V (0 * stale must stay 0)
+        const int valid = t1 - (T + 16 * wave);
+        if (valid < 16) {
+          const uint32_t vblk = st + (4 + wave) * kTileBlock;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int qd = tid + 256 * k;
-        *reinterpret_cast<u32x4*>(lds + (qd >> 4) * kKStride + 16 * (qd & 15)) = kr[k];
-      }
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int qd = tid + 256 * k;
-        const int pr = qd >> 4;
-        const int c = qd & 15;
-        uint8_t* vt = lds + kLdsK + 4 * pr;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t x0 = v0[k][i];
-          const uint32_t x1 = v1[k][i];
-          *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i) * kVStride) = (x0 & 0xffffu) | (x1 << 16);
-          *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i + 1) * kVStride) = (x0 >> 16) | (x1 & 0xffff0000u);
+          for (int u = 0; u < 4; ++u) {
+            const int q = lane + 64 * u;
+            if ((q >> 4) >= valid) lds_zero16(vblk + 16 * q);
+          }
         }
       }
-      __syncthreads();
-      if (T + kTileTokens < t1) gload(T + kTileTokens);
+      __syncthreads();  // every block of the tile is in LDS; the other stage is free
+      if (T + kTileTokens < t1) copy_block(T + kTileTokens, stage ^ 1);
 
       if (wave_on) {
+        const bool full = T + kTileTokens - 1 <= lim_min;
         f32x4 sc[4][2];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
@@ -491,25 +504,24 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
         for (int k = 0; k < 4; ++k)
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb) {
-            const u32x4 kfrag =
-                *reinterpret_cast<const u32x4*>(lds + (16 * tb + L) * kKStride + 64 * k + 16 * J);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) sc[tb][cb] = mfma16<BF16>(kfrag, qf[cb][k], sc[tb][cb]);
+            const u32x4 kf = lds_read16(st + tb * kTileBlock + k_lds[k]);
+            sc[tb][0] = mfma16<BF16>(kf, qf[0][k], sc[tb][0]);
+            if (ncb > 1) sc[tb][1] = mfma16<BF16>(kf, qf[1][k], sc[tb][1]);
           }
 
         u32x4 pf[2][2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
+          if (cb >= ncb) break;
           float x[4][4];
           float mx = kNegInf;
 #pragma unroll
           for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int tok = T + 16 * tb + 4 * J + r;
-              const float v = tok <= lim[cb] ? sc[tb][cb][r] * a.scale_log2 : kNegInf;
-              x[tb][r] = v;
-              mx = fmaxf(mx, v);
+              const float v = sc[tb][cb][r] * a.scale_log2;
+              x[tb][r] = (full || T + 16 * tb + 4 * J + r <= lim[cb]) ? v : kNegInf;
+              mx = fmaxf(mx, x[tb][r]);
             }
           mx = fmaxf(mx, xor16(mx));
           mx = fmaxf(mx, xor32(mx));
@@ -526,8 +538,10 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
             }
           lsum[cb] = lsum[cb] * alpha + ps;
           m[cb] = m_new;
+          if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
 #pragma unroll
-          for (int db = 0; db < 8; ++db) o[db][cb] *= alpha;
+            for (int db = 0; db < 8; ++db) o[db][cb] *= alpha;
+          }
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
             pf[ks][cb][0] = pack2<BF16>(x[2 * ks][0], x[2 * ks][1]);
@@ -537,27 +551,29 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
           }
         }
 
+        const uint32_t vst = st + 4 * kTileBlock;
 #pragma unroll
         for (int db = 0; db < 8; ++db)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            const uint8_t* vb = lds + kLdsK + (16 * db + L) * kVStride + 64 * ks + 8 * J;
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(vb);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(vb + 32);
-            const u32x4 vfrag = {lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) o[db][cb] = mfma16<BF16>(vfrag, pf[ks][cb], o[db][cb]);
+            const u32x2 lo = lds_read_tr16(vst + (2 * ks) * kTileBlock + v_lds[db]);
+            const u32x2 hi = lds_read_tr16(vst + (2 * ks + 1) * kTileBlock + v_lds[db]);
+            const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+            o[db][0] = mfma16<BF16>(vf, pf[ks][0], o[db][0]);
+            if (ncb > 1) o[db][1] = mfma16<BF16>(vf, pf[ks][1], o[db][1]);
           }
       }
+      stage ^= 1;
     }
 
     if (wave_on) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
+        if (cb >= ncb) break;
         float ln = lsum[cb];
         ln += xor16(ln);
         ln += xor32(ln);
-        const int n = 32 * wave + 16 * cb + L;
+        const int n = wave * wcols + 16 * cb + L;
         if (n < ncols) {
           const float inv = ln > 0.f ? 1.f / ln : 0.f;
           const float l2 = ln > 0.f ? m[cb] + __log2f(ln) : kNegInf;
@@ -580,7 +596,7 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
         }
       }
     }
-    __syncthreads();  // LDS reuse by the next item
+    __syncthreads();  // the ring is reused by the next item
   }
 }
 
@@ -676,15 +692,23 @@ hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st)
   return hipGetLastError();
 }
 
-hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st) {
-  if (bf16) {
-    if (causal) hipLaunchKernelGGL((attn_tile_kernel<true, true>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attn_tile_kernel<true, false>), dim3(grid), dim3(256), 0, st, a);
-  } else {
-    if (causal) hipLaunchKernelGGL((attn_tile_kernel<false, true>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attn_tile_kernel<false, false>), dim3(grid), dim3(256), 0, st, a);
+template <bool BF16, bool CAUSAL>
+static hipError_t tile_launch(const AttnArgs& a, int grid, hipStream_t st) {
+  const size_t lds = 2 * kTileStage;
+  static bool lds_ok = false;
+  if (!lds_ok) {
+    const hipError_t e = hipFuncSetAttribute((const void*)attn_tile_kernel<BF16, CAUSAL>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    lds_ok = true;
   }
+  hipLaunchKernelGGL((attn_tile_kernel<BF16, CAUSAL>), dim3(grid), dim3(256), lds, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st) {
+  if (bf16) return causal ? tile_launch<true, true>(a, grid, st) : tile_launch<true, false>(a, grid, st);
+  return causal ? tile_launch<false, true>(a, grid, st) : tile_launch<false, false>(a, grid, st);
 }
 
 }  // namespace feattn

@@ -201,8 +201,9 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
       if (s.qlen * G > kDecodeCols) pairs += (int64_t)ceil_div(s.qlen, qr) * sh.hkv;
     }
     if (pairs == 0) continue;
-    // Aim for >= 2 resident workgroups per compute unit; never split below 256 tokens.
-    int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 2 + pairs - 1) / pairs);
+    // Aim for about 8 items per compute unit (2 resident workgroups, several
+    // rounds in longest-first order); never split below 256 tokens.
+    int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 8 + pairs - 1) / pairs);
     for (;;) {
       ml.tile.clear();
       ml.merge.clear();
