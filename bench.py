@@ -101,17 +101,38 @@ def decode_headline(steps, warmup, dev):
     return b, ms, nbytes
 
 
-def secondary(dev):
-    """Other workload shapes: ms per call and throughput."""
+def secondary(dev, only=None):
+    """Other workload shapes: ms per call and throughput.  `only` selects one
+    of prefill / dflash / mixed / long."""
     import torch
 
     import feattn
     from feattn import workloads as W
 
     res = {}
+    want = lambda name: only is None or only == name
 
     # chunked prefill (causal within chunk, full over prefix) + fused RoPE/append
     b = W.qwen3_8b_prefill()
+    if not want("prefill"):
+        b = None
+    if b is not None:
+        _prefill(b, dev, res)
+    if want("dflash"):
+        _dflash(dev, res)
+    if want("mixed"):
+        _mixed(dev, res)
+    if want("long"):
+        _long(dev, res)
+    return res
+
+
+def _prefill(b, dev, res):
+    import torch
+
+    import feattn
+    from feattn import workloads as W
+
     plan, step = attn_setup(b, dev, torch.bfloat16, True, 1)
     ms = event_time_ms(step, 20, 3)
     flops = W.attention_flops(b, True)
@@ -135,7 +156,12 @@ def secondary(dev):
         "rope_append_ms": round(ms_ra, 4),
         "rope_append_gbs": round(W.rope_append_bytes(b) / ms_ra / 1e6, 1)}
     log("prefill", res["prefill_qwen3_8b"])
-    del kc, vc
+
+
+def _dflash(dev, res):
+    import torch
+
+    from feattn import workloads as W
 
     # DFlash non-causal 16-row blocks, bf16 and fp16
     for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
@@ -150,6 +176,12 @@ def secondary(dev):
             "tflops": round(flops / ms / 1e9, 2)}
         plan.close()
         log("dflash", name, res[f"dflash_block_{name}"])
+
+
+def _mixed(dev, res):
+    import torch
+
+    from feattn import workloads as W
 
     # mixed decode + prefill (Qwen3-30B-A3B heads: 32 q / 4 kv)
     b = W.qwen3_30b_mixed()
@@ -170,6 +202,12 @@ def secondary(dev):
     plan.close()
     log("mixed", res["mixed_qwen3_30b"])
 
+
+def _long(dev, res):
+    import torch
+
+    from feattn import workloads as W
+
     # long-context decode (split-KV)
     b = W.long_decode()
     plan, step = attn_setup(b, dev, torch.bfloat16, True, 1)
@@ -178,7 +216,6 @@ def secondary(dev):
                               "gbs": round(W.decode_bytes(b) / ms / 1e6, 1)}
     plan.close()
     log("long", res["long_decode_32k"])
-    return res
 
 
 def copy_calibration(dev, mib=1024):
@@ -235,6 +272,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long"],
+                    help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the attention path has no multi-GPU mode in this "
@@ -250,6 +289,9 @@ def main():
     torch.cuda.set_device(dev)
     feattn.lib()
     log("library", feattn.version())
+    if args.only:
+        print(json.dumps(secondary(dev, args.only)), flush=True)
+        return
 
     b, ms, nbytes = decode_headline(args.steps, args.warmup, dev)
     gbs = nbytes / ms / 1e6

@@ -362,7 +362,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 // the next tile's copy is issued and the current tile is computed.
 //
 // Columns: an item of <= 64 (query row, head) columns gives each wavefront
-// one 16-column block, a larger item (<= 128) two.  Per wavefront and tile:
+// NCB = 1 block of 16 columns, a larger item (<= 128) NCB = 2.  The item
+// body is instantiated per NCB, and per tile for masked (diagonal / last)
+// and unmasked tiles, so the unrolled MFMA sequences carry no branches.
+// Per wavefront and tile:
 //   S^T = K Q^T: A = K rows from LDS (lane: token 16tb+L, dims 32s+8J..+8),
 //                B = Q^T in registers; C: lane holds tokens 16tb+4J+r of
 //                column L.
@@ -374,6 +377,212 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 constexpr int kTileBlock = 4096;               // 16 tokens x 256 bytes
 constexpr int kTileStage = 8 * kTileBlock;     // K blocks 0..3, then V blocks 0..3
 
+struct TileLanes {
+  int k_goff[4], v_goff[4];
+  uint32_t k_lds[4], v_lds[8];
+};
+
+template <bool BF16, bool CAUSAL, int NCB>
+__device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, const SeqInfo& s,
+                                          const TileLanes& tl, uint32_t lbase, int wave, int lane) {
+  const int J = lane >> 4;
+  const int L = lane & 15;
+  const int G = a.group;
+  const int pshift = a.page_shift;
+  const int pmask = (1 << pshift) - 1;
+  const int row_bytes = a.hkv * kHeadDim * 2;
+  const int kvh = w.kvh;
+  const int t0 = w.t0;
+  const int t1 = w.t1;
+  const int ncols = w.nq * G;
+  constexpr int kWcols = 16 * NCB;  // columns per wavefront
+  const bool wave_on = wave * kWcols < ncols;
+
+  // This wavefront's block of a tile: K and V rows [T + 16 wave, +16).
+  const char* kb0 = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
+  const char* vb0 = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
+  auto copy_block = [&](int T, int stage) {
+    const int tok = T + 16 * wave;
+    if (tok >= t1) return;
+    const int pg = ldc(a.pages, s.page_off + (tok >> pshift));
+    const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
+    const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lds_dma16(kb0 + blk + tl.k_goff[r], st + wave * kTileBlock + 1024 * r);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lds_dma16(vb0 + blk + tl.v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
+  };
+
+  wait_lds();
+  copy_block(t0, 0);
+
+  int lim[NCB], crow[NCB], chead[NCB];
+  u32x4 qf[NCB][4];
+  int lim_min = 1 << 30;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int n = wave * kWcols + 16 * cb + L;
+    const bool ok = n < ncols;
+    crow[cb] = w.q0 + (ok ? n / G : 0);
+    chead[cb] = kvh * G + (ok ? n % G : 0);
+    lim[cb] = -1;
+    if (ok) lim[cb] = min(CAUSAL ? s.len - s.qlen + (crow[cb] - s.qo) : s.len - 1, t1 - 1);
+    if (ok) lim_min = min(lim_min, lim[cb]);
+    const uint16_t* qp = a.q + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 8 * J;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qf[cb][k] = ld16(qp + 32 * k);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (!ok) qf[cb][k] = u32x4{0u, 0u, 0u, 0u};
+      // Q (and the first tile's copy, issued before it) have landed past this
+      // point; the registers are then plain values, so no wait for them falls
+      // inside the tile loop while the next copy is in flight.
+      asm volatile("" : "+v"(qf[cb][k]));
+    }
+  }
+  // Tiles ending at or before every column's limit of the wavefront need no mask.
+#pragma unroll
+  for (int o_ = 32; o_ >= 1; o_ >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o_, 64));
+
+  float m[NCB], lsum[NCB];
+  f32x4 o[8][NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    m[cb] = kNegInf;
+    lsum[cb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[db][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto compute = [&](uint32_t st, int T, auto masked) {
+    constexpr bool MASK = decltype(masked)::value;
+    f32x4 sc[4][NCB];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) sc[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const u32x4 kf = lds_read16(st + tb * kTileBlock + tl.k_lds[k]);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) sc[tb][cb] = mfma16<BF16>(kf, qf[cb][k], sc[tb][cb]);
+      }
+
+    u32x4 pf[2][NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      // Row max on raw scores (the scale is positive), then
+      // p = exp2(s * scale - max * scale) with one FMA per element.
+      float mx = kNegInf;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (MASK) {
+            if (T + 16 * tb + 4 * J + r > lim[cb]) sc[tb][cb][r] = kNegInf;
+          }
+          mx = fmaxf(mx, sc[tb][cb][r]);
+        }
+      mx = fmaxf(mx, xor16(mx));
+      mx = fmaxf(mx, xor32(mx));
+      const float m_new = fmaxf(m[cb], mx * a.scale_log2);
+      const float m_use = m_new == kNegInf ? 0.f : m_new;
+      const float alpha = fast_exp2(m[cb] - m_use);
+      float x[4][4];
+      float ps = 0.f;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[tb][r] = fast_exp2(__builtin_fmaf(sc[tb][cb][r], a.scale_log2, -m_use));
+          ps += x[tb][r];
+        }
+      lsum[cb] = lsum[cb] * alpha + ps;
+      m[cb] = m_new;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db][cb] *= alpha;
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        pf[ks][cb][0] = pack2<BF16>(x[2 * ks][0], x[2 * ks][1]);
+        pf[ks][cb][1] = pack2<BF16>(x[2 * ks][2], x[2 * ks][3]);
+        pf[ks][cb][2] = pack2<BF16>(x[2 * ks + 1][0], x[2 * ks + 1][1]);
+        pf[ks][cb][3] = pack2<BF16>(x[2 * ks + 1][2], x[2 * ks + 1][3]);
+      }
+    }
+
+    const uint32_t vst = st + 4 * kTileBlock;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x2 lo = lds_read_tr16(vst + (2 * ks) * kTileBlock + tl.v_lds[db]);
+        const u32x2 hi = lds_read_tr16(vst + (2 * ks + 1) * kTileBlock + tl.v_lds[db]);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) o[db][cb] = mfma16<BF16>(vf, pf[ks][cb], o[db][cb]);
+      }
+  };
+
+  int stage = 0;
+  for (int T = t0; T < t1; T += kTileTokens) {
+    wait_vmem<0>();  // this wavefront's block of the tile has landed
+    const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
+    {
+      // rows at or past the item end: zero V (0 * stale must stay 0)
+      const int valid = t1 - (T + 16 * wave);
+      if (valid < 16) {
+        const uint32_t vblk = st + (4 + wave) * kTileBlock;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int q = lane + 64 * u;
+          if ((q >> 4) >= valid) lds_zero16(vblk + 16 * q);
+        }
+      }
+    }
+    __syncthreads();  // every block of the tile is in LDS; the other stage is free
+    if (T + kTileTokens < t1) copy_block(T + kTileTokens, stage ^ 1);
+    if (wave_on) {
+      if (T + kTileTokens - 1 <= lim_min) compute(st, T, std::false_type{});
+      else compute(st, T, std::true_type{});
+    }
+    stage ^= 1;
+  }
+
+  if (wave_on) {
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      float ln = lsum[cb];
+      ln += xor16(ln);
+      ln += xor32(ln);
+      const int n = wave * kWcols + 16 * cb + L;
+      if (n < ncols) {
+        const float inv = ln > 0.f ? 1.f / ln : 0.f;
+        const float l2 = ln > 0.f ? m[cb] + __log2f(ln) : kNegInf;
+        if (w.part < 0) {
+          uint16_t* op = a.out + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 4 * J;
+#pragma unroll
+          for (int db = 0; db < 8; ++db) {
+            u32x2 v = {pack2<BF16>(o[db][cb][0] * inv, o[db][cb][1] * inv),
+                       pack2<BF16>(o[db][cb][2] * inv, o[db][cb][3] * inv)};
+            *reinterpret_cast<u32x2*>(op + 16 * db) = v;
+          }
+          if (a.lse != nullptr && J == 0) a.lse[(size_t)crow[cb] * a.hq + chead[cb]] = l2 * kLn2;
+        } else {
+          const size_t slot = (size_t)(w.part + (n / G));
+          float* po = a.part_o + (slot * a.hq + chead[cb]) * kHeadDim + 4 * J;
+#pragma unroll
+          for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db][cb] * inv;
+          if (J == 0) a.part_lse[slot * a.hq + chead[cb]] = l2;
+        }
+      }
+    }
+  }
+}
+
 template <bool BF16, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
@@ -383,219 +592,32 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
   const int J = lane >> 4;
   const int L = lane & 15;
   const int n_items = uniform(*a.n_items);
-  const int G = a.group;
-  const int pshift = a.page_shift;
-  const int pmask = (1 << pshift) - 1;
   const int row_bytes = a.hkv * kHeadDim * 2;
   const uint32_t lbase = (uint32_t)(uintptr_t)dsm;
 
-  int k_goff[4], v_goff[4];
+  TileLanes tl;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = 4 * r + J;
-    k_goff[r] = t * row_bytes + 16 * (L ^ t);
-    v_goff[r] = t * row_bytes + 16 * (L ^ ((2 * t) & 15));
+    tl.k_goff[r] = t * row_bytes + 16 * (L ^ t);
+    tl.v_goff[r] = t * row_bytes + 16 * (L ^ ((2 * t) & 15));
   }
-  uint32_t k_lds[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) k_lds[s] = (uint32_t)(16 * (16 * L + (((4 * s + J) ^ L) & 15)));
-  uint32_t v_lds[8];
+  for (int s = 0; s < 4; ++s) tl.k_lds[s] = (uint32_t)(16 * (16 * L + (((4 * s + J) ^ L) & 15)));
   {
     const int k = L >> 2, m = L & 3, t = 4 * J + k;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const int c = 2 * db + (m >> 1);
-      v_lds[db] = (uint32_t)(16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
+      tl.v_lds[db] = (uint32_t)(16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
     }
   }
 
   for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
     const WorkItem w = ldc_item(a.items, it);
     const SeqInfo s = ldc_seq(a.seqs, w.seq);
-    const int kvh = w.kvh;
-    const int t0 = w.t0;
-    const int t1 = w.t1;
-    const int ncols = w.nq * G;
-    const int wcols = ncols <= 64 ? 16 : 32;  // columns per wavefront
-    const int ncb = wcols / 16;
-    const bool wave_on = wave * wcols < ncols;
-
-    // This wavefront's block of a tile: K and V rows [T + 16 wave, +16).
-    const char* kb0 = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
-    const char* vb0 = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
-    auto copy_block = [&](int T, int stage) {
-      const int tok = T + 16 * wave;
-      if (tok >= t1) return;
-      const int pg = ldc(a.pages, s.page_off + (tok >> pshift));
-      const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
-      const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(kb0 + blk + k_goff[r], st + wave * kTileBlock + 1024 * r);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(vb0 + blk + v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
-    };
-
-    wait_lds();
-    copy_block(t0, 0);
-
-    int lim[2], crow[2], chead[2];
-    u32x4 qf[2][4];
-    int lim_min = 1 << 30;
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int n = wave * wcols + 16 * cb + L;
-      const bool ok = cb < ncb && n < ncols;
-      crow[cb] = w.q0 + (ok ? n / G : 0);
-      chead[cb] = kvh * G + (ok ? n % G : 0);
-      lim[cb] = -1;
-      if (ok) lim[cb] = min(CAUSAL ? s.len - s.qlen + (crow[cb] - s.qo) : s.len - 1, t1 - 1);
-      if (ok) lim_min = min(lim_min, lim[cb]);
-      const uint16_t* qp = a.q + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 8 * J;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) qf[cb][k] = ld16(qp + 32 * k);
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (!ok) qf[cb][k] = u32x4{0u, 0u, 0u, 0u};
-    }
-    // Q (and the first tile's copy, issued before it) have landed once this
-    // returns; afterwards the registers are plain values, so no wait for them
-    // falls inside the tile loop while the next copy is in flight.
-    asm volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[0][2]), "+v"(qf[0][3]), "+v"(qf[1][0]),
-                 "+v"(qf[1][1]), "+v"(qf[1][2]), "+v"(qf[1][3]));
-    // Tiles ending at or before every column's limit need no mask.
-#pragma unroll
-    for (int o_ = 32; o_ >= 1; o_ >>= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o_, 64));
-
-    float m[2] = {kNegInf, kNegInf};
-    float lsum[2] = {0.f, 0.f};
-    f32x4 o[8][2];
-#pragma unroll
-    for (int db = 0; db < 8; ++db)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) o[db][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    int stage = 0;
-    for (int T = t0; T < t1; T += kTileTokens) {
-      wait_vmem<0>();  // this wavefront's block of the tile has landed
-      const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
-      {
-        // rows at or past the item end: zero V (0 * stale must stay 0)
-        const int valid = t1 - (T + 16 * wave);
-        if (valid < 16) {
-          const uint32_t vblk = st + (4 + wave) * kTileBlock;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int q = lane + 64 * u;
-            if ((q >> 4) >= valid) lds_zero16(vblk + 16 * q);
-          }
-        }
-      }
-      __syncthreads();  // every block of the tile is in LDS; the other stage is free
-      if (T + kTileTokens < t1) copy_block(T + kTileTokens, stage ^ 1);
-
-      if (wave_on) {
-        const bool full = T + kTileTokens - 1 <= lim_min;
-        f32x4 sc[4][2];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) sc[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) {
-            const u32x4 kf = lds_read16(st + tb * kTileBlock + k_lds[k]);
-            sc[tb][0] = mfma16<BF16>(kf, qf[0][k], sc[tb][0]);
-            if (ncb > 1) sc[tb][1] = mfma16<BF16>(kf, qf[1][k], sc[tb][1]);
-          }
-
-        u32x4 pf[2][2];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          if (cb >= ncb) break;
-          float x[4][4];
-          float mx = kNegInf;
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float v = sc[tb][cb][r] * a.scale_log2;
-              x[tb][r] = (full || T + 16 * tb + 4 * J + r <= lim[cb]) ? v : kNegInf;
-              mx = fmaxf(mx, x[tb][r]);
-            }
-          mx = fmaxf(mx, xor16(mx));
-          mx = fmaxf(mx, xor32(mx));
-          const float m_new = fmaxf(m[cb], mx);
-          const float m_use = m_new == kNegInf ? 0.f : m_new;
-          const float alpha = fast_exp2(m[cb] - m_use);
-          float ps = 0.f;
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              x[tb][r] = fast_exp2(x[tb][r] - m_use);
-              ps += x[tb][r];
-            }
-          lsum[cb] = lsum[cb] * alpha + ps;
-          m[cb] = m_new;
-          if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
-#pragma unroll
-            for (int db = 0; db < 8; ++db) o[db][cb] *= alpha;
-          }
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            pf[ks][cb][0] = pack2<BF16>(x[2 * ks][0], x[2 * ks][1]);
-            pf[ks][cb][1] = pack2<BF16>(x[2 * ks][2], x[2 * ks][3]);
-            pf[ks][cb][2] = pack2<BF16>(x[2 * ks + 1][0], x[2 * ks + 1][1]);
-            pf[ks][cb][3] = pack2<BF16>(x[2 * ks + 1][2], x[2 * ks + 1][3]);
-          }
-        }
-
-        const uint32_t vst = st + 4 * kTileBlock;
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const u32x2 lo = lds_read_tr16(vst + (2 * ks) * kTileBlock + v_lds[db]);
-            const u32x2 hi = lds_read_tr16(vst + (2 * ks + 1) * kTileBlock + v_lds[db]);
-            const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
-            o[db][0] = mfma16<BF16>(vf, pf[ks][0], o[db][0]);
-            if (ncb > 1) o[db][1] = mfma16<BF16>(vf, pf[ks][1], o[db][1]);
-          }
-      }
-      stage ^= 1;
-    }
-
-    if (wave_on) {
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        if (cb >= ncb) break;
-        float ln = lsum[cb];
-        ln += xor16(ln);
-        ln += xor32(ln);
-        const int n = wave * wcols + 16 * cb + L;
-        if (n < ncols) {
-          const float inv = ln > 0.f ? 1.f / ln : 0.f;
-          const float l2 = ln > 0.f ? m[cb] + __log2f(ln) : kNegInf;
-          if (w.part < 0) {
-            uint16_t* op = a.out + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 4 * J;
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-              u32x2 v = {pack2<BF16>(o[db][cb][0] * inv, o[db][cb][1] * inv),
-                         pack2<BF16>(o[db][cb][2] * inv, o[db][cb][3] * inv)};
-              *reinterpret_cast<u32x2*>(op + 16 * db) = v;
-            }
-            if (a.lse != nullptr && J == 0) a.lse[(size_t)crow[cb] * a.hq + chead[cb]] = l2 * kLn2;
-          } else {
-            const size_t slot = (size_t)(w.part + (n / G));
-            float* po = a.part_o + (slot * a.hq + chead[cb]) * kHeadDim + 4 * J;
-#pragma unroll
-            for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db][cb] * inv;
-            if (J == 0) a.part_lse[slot * a.hq + chead[cb]] = l2;
-          }
-        }
-      }
-    }
+    if (w.nq * a.group <= 64) tile_item<BF16, CAUSAL, 1>(a, w, s, tl, lbase, wave, lane);
+    else tile_item<BF16, CAUSAL, 2>(a, w, s, tl, lbase, wave, lane);
     __syncthreads();  // the ring is reused by the next item
   }
 }
