@@ -38,6 +38,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per decode step (decode kernel + split-KV merge) from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload,
+    calibrated against a 1 GiB copy; None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_qwen3_8b_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("decode_step_traffic_bytes"):
+            return int(float(line.split("=")[1]))
+    return None
+
+
 def event_time_ms(fn, iters, warmup):
     """Average ms per call of fn() over `iters` calls, timed with events on
     the current stream (the stream the library launches on)."""
@@ -276,8 +289,8 @@ def main():
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: the attention path has no multi-GPU mode in this "
-              "build (sequences and kv heads shard without exchange; see DESIGN.md)",
+        print("bench.py measures one GPU: this attention library has no multi-GPU mode "
+              "(sequences and kv heads shard across GPUs without any exchange)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -311,9 +324,12 @@ def main():
                                "KV pools",
                    "batch": b.batch, "context_tokens": sum(b.lens), "pages": b.blocks},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes,
-                     "timed": "fe_attn_run (decode kernel + split-KV merge), HIP events"},
+                     "timed": "one fe_attn_run per step (attn_decode_kernel + attn_merge_kernel, "
+                              "the whole attention call), HIP events on the launch stream; traffic "
+                              "from profiles/decode_qwen3_8b_hbm_traffic.txt"},
         "cpu_baseline": cpu,
         "secondary": sec,
     }
