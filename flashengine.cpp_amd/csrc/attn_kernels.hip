@@ -8,16 +8,17 @@
 // units internally and converted to natural log on output.
 //
 // Three kernels:
-//  * attn_decode_kernel: one wavefront per work item of at most 16
-//    (query row, head) columns (decode rows, GQA heads packed along the MFMA
-//    N dimension).  K streams straight from HBM into MFMA A-operand registers
-//    (S^T = K Q^T); P.V runs on the VALU with coalesced 256-byte V row loads.
-//  * attn_tile_kernel: four wavefronts share 64-token K / V^T tiles staged in
-//    LDS; each wavefront owns 32 (query row, head) columns and computes
-//    S^T = K Q^T and O^T = V^T P^T on the bf16/fp16 MFMA with fp32
+//  * attn_decode_kernel: persistent; each wavefront walks one share of the
+//    decode token stream for one kv head (pieces of <= 16 (query row, head)
+//    columns: decode rows x GQA heads along the MFMA N dimension), copying
+//    Q / K / V units straight into a small LDS ring and computing
+//    S^T = K Q^T and O^T = V^T P^T on the MFMA.
+//  * attn_tile_kernel: four wavefronts share 64-token K / V tiles staged in
+//    LDS; each wavefront owns 16 or 32 (query row, head) columns and
+//    computes S^T = K Q^T and O^T = V^T P^T on the bf16/fp16 MFMA with fp32
 //    accumulation (chunked prefill, DFlash blocks, verify rows).
 //  * attn_merge_kernel: combines split-KV partials by their log-sum-exp, one
-//    wavefront per (query row, head) with every split's loads in flight.
+//    wavefront per (query row, head) with a batch of splits in flight.
 #include <type_traits>
 
 #include "attn_types.hpp"
@@ -42,15 +43,15 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
 // runs, so wave-uniform indices become scalar loads.
 typedef const __attribute__((address_space(4))) int32_t* const_i32p;
 
-__device__ __forceinline__ int32_t ldc(const int32_t* p, size_t i) { return ((const_i32p)p)[i]; }
+__device__ __forceinline__ int32_t ldc(const int32_t* p, int i) { return ((const_i32p)p)[uniform(i)]; }
 
 __device__ __forceinline__ WorkItem ldc_item(const WorkItem* items, int i) {
-  const int32_t* p = reinterpret_cast<const int32_t*>(items + i);
+  const int32_t* p = reinterpret_cast<const int32_t*>(items + uniform(i));
   return WorkItem{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3), ldc(p, 4), ldc(p, 5), ldc(p, 6), ldc(p, 7)};
 }
 
 __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
-  const int32_t* p = reinterpret_cast<const int32_t*>(seqs + i);
+  const int32_t* p = reinterpret_cast<const int32_t*>(seqs + uniform(i));
   return SeqInfo{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3)};
 }
 
@@ -64,15 +65,16 @@ __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
 // of a workgroup stream the same cache pages together.
 //
 // HBM -> LDS copies use direct-to-LDS loads (global_load_lds_dwordx4: lane i
-// of an instruction lands at LDS base + 16 i).  Each wavefront owns a
-// two-stage ring (one 16-token block of K then V per stage) and a Q buffer.
-// The copy of the next block -- at an item's last block, the next item's Q
-// and first block -- is in flight while the current block is computed, so
-// item boundaries do not drain the pipeline.  Every copy instruction moves
-// four whole 256-byte rows; inside a stage, 16-byte chunk c of row t sits at
-// chunk position c ^ t (K, Q) or c ^ (2t mod 16) (V), which makes the operand
-// reads below free of LDS bank conflicts.  Page ids are read with scalar
-// loads one block ahead of their use.
+// of an instruction lands at LDS base + 16 i).  A wavefront's share is one
+// stream of 4 KB units -- per item: its Q (16 columns x 256 bytes), then
+// K and V of each 16-token block -- copied into a ring of U unit slots that
+// the wavefront owns.  Copies run up to U units ahead of the unit being
+// computed, across item boundaries, so a wavefront keeps U - 2 units in
+// flight while it computes.  Every copy instruction moves
+// four whole 256-byte rows; inside a unit, 16-byte chunk c of row t sits at
+// chunk position c ^ t (K, Q) or c ^ (2t mod 16) (V), which makes the
+// operand reads below free of LDS bank conflicts.  Page ids and item
+// metadata are read with scalar loads one block / one item ahead of use.
 //
 // Lane = 16*J + L.  Per block:
 //   S^T = K Q^T:  A = K rows (lane: token L, dims 32s+8J..+8, ds_read_b128),
@@ -83,9 +85,20 @@ __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
 //                 4J..4J+3 = its own S^T values), 8 x 16x16x16 MFMA;
 //                 C: lane holds dims 16db+4J+r of column L.
 // Softmax statistics are per column, i.e. per lane (reduced over J).
-constexpr int kDecStage = 8192;                        // one 16-token block: K (4 KB) then V (4 KB)
-constexpr int kDecQ = 4096;                            // Q of one item: 16 columns x 256 bytes
-constexpr int kDecWaveLds = 2 * kDecStage + kDecQ;     // per wavefront
+constexpr int kDecUnit = 4096;  // 16 rows x 256 bytes: one K or V block, or one item's Q
+constexpr int kLdsBytes = 163840;
+
+// Ring slots per wavefront.  Three (one unit in flight while a K/V pair is
+// computed) measured fastest: with 8 wavefronts per CU, deeper rings only
+// add queueing in the memory system.
+#ifndef FEATTN_DECODE_UNITS
+#define FEATTN_DECODE_UNITS 3
+#endif
+template <int WAVES>
+constexpr int dec_units() {
+  static_assert(FEATTN_DECODE_UNITS * WAVES * kDecUnit <= kLdsBytes, "decode ring exceeds LDS");
+  return FEATTN_DECODE_UNITS;
+}
 
 __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
   uint32_t saved;
@@ -95,13 +108,28 @@ __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) 
       "global_load_lds_dwordx4 %1, off\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(gaddr), "s"(lds_addr)
+      : "v"(gaddr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))  // wave-uniform by construction
       : "memory");
 }
 
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Waits until at most `n` units (4 copy instructions each) issued after the
+// awaited one are still in flight; n is wave-uniform.  vmcnt holds 6 bits,
+// so n is clamped to 15 (a longer wait, never a shorter one).
+template <int MAXU>
+__device__ __forceinline__ void wait_units(int n) {
+  static_for<0, (MAXU < 15 ? MAXU : 15) + 1>([&](auto i) {
+    constexpr int I = decltype(i)::value;
+    if (I == (MAXU < 15 ? MAXU : 15)) {
+      if (n >= I) wait_vmem<4 * I>();
+    } else if (n == I) {
+      wait_vmem<4 * I>();
+    }
+  });
 }
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -136,19 +164,49 @@ __device__ __forceinline__ void lds_zero16(uint32_t lds_addr) {
   *(lds_u32x4*)(uintptr_t)lds_addr = u32x4{0u, 0u, 0u, 0u};
 }
 
+__device__ __forceinline__ DecodeItem ldc_ditem(const DecodeItem* items, int i) {
+  const int32_t* p = reinterpret_cast<const int32_t*>(items + uniform(i));
+  return DecodeItem{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3), ldc(p, 4), ldc(p, 5), ldc(p, 6), ldc(p, 7)};
+}
+
+__device__ __forceinline__ ShareStart ldc_share(const ShareStart* shares, int i) {
+  typedef const __attribute__((address_space(4))) i32x16* const_i32x16p;
+  const i32x16 v = *(const_i32x16p)(shares + uniform(i));
+  ShareStart r;
+  r.it_begin = v[0];
+  r.it_end = v[1];
+  r.first = DecodeItem{v[2], v[3], v[4], v[5], v[6], v[7], v[8], v[9]};
+  r.pg0 = v[10];
+  r.pg1 = v[11];
+  return r;
+}
+
 template <bool BF16, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int causal) {
+  constexpr int U = dec_units<WAVES>();
+  static_assert(U >= 2, "the ring must hold one K/V pair");
   extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
   const int lane = threadIdx.x & 63;
   const int J = lane >> 4;
   const int L = lane & 15;
   const int wave = uniform(threadIdx.x >> 6);
-  const int n_items = uniform(*a.n_items);
   const int G = a.group;
   const int pshift = a.page_shift;
   const int pmask = (1 << pshift) - 1;
-  const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * kDecWaveLds);
-  const uint32_t qbuf = ring + 2 * kDecStage;
+  const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * U * kDecUnit);
+
+  // Wavefront slot -> (kv head, share): consecutive slots are consecutive
+  // kv heads of one share (WAVES divides hkv, so a workgroup holds one
+  // share and its wavefronts walk the same blocks).  Records past the
+  // shares in use are empty.
+  const int slot = blockIdx.x * WAVES + wave;
+  const int kvh = slot % a.hkv;
+  const int share = slot / a.hkv;
+  if (share >= a.n_share_cap) return;
+  const ShareStart rec = ldc_share(a.shares, share);
+  const int it_begin = rec.it_begin;
+  const int it_end = rec.it_end;
+  if (it_begin >= it_end) return;
 
   // Per-lane pieces of the copy and read addresses (fixed for the kernel).
   // Copy instruction r, lane i = 16*J + L: row 4r + J, chunk position L.
@@ -172,62 +230,99 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const int c = 2 * db + (m >> 1);
-      v_lds[db] = (uint32_t)(4096 + 16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
+      v_lds[db] = (uint32_t)(16 * (16 * t + ((c ^ (2 * t)) & 15)) + 8 * (m & 1));
     }
   }
 
-  // Wavefront slot -> (kv head, share): consecutive slots are consecutive
-  // kv heads of one share.  n_items counts the shares in use.
-  const int slot = blockIdx.x * WAVES + wave;
-  if (slot >= n_items * a.hkv) return;
-  const int kvh = slot % a.hkv;
-  const int share = slot / a.hkv;
-  int it = ldc(a.share_off, share);
-  const int it_end = ldc(a.share_off, share + 1);
-  if (it >= it_end) return;
-
-  auto page_id = [&](const SeqInfo& sq, int tok) { return ldc(a.pages, sq.page_off + (tok >> pshift)); };
-  // Copies one 16-token block of this wavefront's kv head into ring stage `stage`.
-  auto copy_block = [&](int tok, int pg, int stage) {
+  const size_t head_off = (size_t)kvh * kHeadDim * 2;
+  auto page_id = [&](const DecodeItem& d, int tok) { return ldc(a.pages, d.page_off + (tok >> pshift)); };
+  auto block_addr = [&](const void* cache, int tok, int pg) {
     const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
-    const char* kb = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2 + blk;
-    const char* vb = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2 + blk;
-    const uint32_t st = ring + (uint32_t)(stage * kDecStage);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lds_dma16(kb + k_goff[r], st + 1024 * r);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lds_dma16(vb + v_goff[r], st + 4096 + 1024 * r);
-  };
-  // Copies the 16 Q^T columns of an item (columns past nq*G repeat column 0).
-  auto copy_q = [&](const WorkItem& wi) {
-    const int nc = wi.nq * G;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = 4 * r + J;
-      const int nn = n < nc ? n : 0;
-      const int row = wi.q0 + nn / G;
-      const int head = kvh * G + nn % G;
-      lds_dma16(a.q + ((size_t)row * a.hq + head) * kHeadDim + 8 * (L ^ n), qbuf + 1024 * r);
-    }
+    return reinterpret_cast<const char*>(cache) + head_off + blk;
   };
 
-  WorkItem w = ldc_item(a.items, it);
-  SeqInfo s = ldc_seq(a.seqs, w.seq);
-  copy_q(w);
-  copy_block(w.t0, page_id(s, w.t0), 0);
-  int stage = 0;
-  // Page id of the block the next copy will fetch; -1 = not yet read.
-  int pg_next = w.t0 + 16 < w.t1 ? page_id(s, w.t0 + 16) : -1;
+  // ---- copy side: the next unit of the share's stream --------------------
+  // kind 0 = Q of item c_it, 1 = K / 2 = V of block c_tok.  The following
+  // item (nw) and the next K block's page id (pg_next) are requested one
+  // item / one block before they are needed; the share record supplies the
+  // first two page ids.
+  int c_it = it_begin;
+  DecodeItem cw = rec.first;
+  DecodeItem nw = cw;
+  if (c_it + 1 < it_end) nw = ldc_ditem(a.ditems, c_it + 1);
+  int c_kind = 0;
+  int c_tok = cw.t0;
+  int pg_next = rec.pg0;
+  int pg_after = rec.pg1;  // page of the block after pg_next's, valid while first_k
+  bool first_k = true;
+  int pg_cur = pg_next;
+  bool c_live = true;
+  int issued = 0;  // units copied so far
+  int c_slot = 0;  // ring slot of the next copy
 
-  for (;;) {
-    const int nit = it + 1;
-    const bool has_next = nit < it_end;
-    WorkItem wn = w;
-    SeqInfo sn = s;
-    if (has_next) {
-      wn = ldc_item(a.items, nit);
-      sn = ldc_seq(a.seqs, wn.seq);
+  auto issue_one = [&]() {
+    const uint32_t dst = ring + (uint32_t)(c_slot * kDecUnit);
+    if (c_kind == 0) {
+      const int nc = cw.nq * G;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = 4 * r + J;
+        const int nn = n < nc ? n : 0;  // columns past the item repeat column 0
+        const int row = cw.q0 + nn / G;
+        const int head = kvh * G + nn % G;
+        lds_dma16(a.q + ((size_t)row * a.hq + head) * kHeadDim + 8 * (L ^ n), dst + 1024 * r);
+      }
+      c_kind = 1;
+    } else if (c_kind == 1) {
+      pg_cur = pg_next;
+      const char* kb = block_addr(a.kc, c_tok, pg_cur);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(kb + k_goff[r], dst + 1024 * r);
+      // page of the next K block: later in this item, or the next item's first
+      if (first_k) {
+        pg_next = pg_after;
+        first_k = false;
+      } else if (c_tok + 16 < cw.t1) {
+        pg_next = page_id(cw, c_tok + 16);
+      } else if (c_it + 1 < it_end) {
+        pg_next = page_id(nw, nw.t0);
+      }
+      c_kind = 2;
+    } else {
+      const char* vb = block_addr(a.vc, c_tok, pg_cur);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_dma16(vb + v_goff[r], dst + 1024 * r);
+      c_tok += 16;
+      c_kind = 1;
+      if (c_tok >= cw.t1) {
+        ++c_it;
+        if (c_it < it_end) {
+          cw = nw;
+          c_tok = cw.t0;
+          c_kind = 0;
+          if (c_it + 1 < it_end) nw = ldc_ditem(a.ditems, c_it + 1);
+        } else {
+          c_live = false;
+        }
+      }
     }
+    ++issued;
+    c_slot = c_slot + 1 == U ? 0 : c_slot + 1;
+  };
+
+  // ---- compute side --------------------------------------------------------
+  int consumed = 0;  // units whose reads are complete
+  int r_slot = 0;    // ring slot of the next unit to compute on
+  // Refills every free slot; the slots freed last were read one step ago.
+  auto refill = [&]() {
+    wait_lds();
+    while (c_live && issued - consumed < U) issue_one();
+  };
+
+  for (int it = it_begin; it < it_end; ++it) {
+    refill();
+    // the copy side read this item's record before (a scalar cache hit)
+    const DecodeItem w = it == it_begin ? rec.first : ldc_ditem(a.ditems, it);
     const int t0 = w.t0;
     const int t1 = w.t1;
     const int ncols = w.nq * G;
@@ -236,19 +331,23 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
     const int chead = kvh * G + (col_ok ? L % G : 0);
     int lim = -1;  // last visible token of column L
     if (col_ok) {
-      lim = causal ? s.len - s.qlen + (crow - s.qo) : s.len - 1;
+      lim = causal ? w.len - w.nq + (crow - w.q0) : w.len - 1;
       lim = min(lim, t1 - 1);
     }
 
-    // This item's Q was copied before its first block: at most the 8 block
-    // copies (and younger stores) may still be outstanding.
-    wait_vmem<8>();
+    // Q unit
+    wait_units<U>(issued - consumed - 1);
     u32x4 qf[4];
+    {
+      const uint32_t qb = ring + (uint32_t)(r_slot * kDecUnit);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      qf[k] = lds_read16(qbuf + k_lds[k]);
-      if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
+      for (int k = 0; k < 4; ++k) {
+        qf[k] = lds_read16(qb + k_lds[k]);
+        if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
+      }
     }
+    consumed += 1;
+    r_slot = r_slot + 1 == U ? 0 : r_slot + 1;
 
     float m = kNegInf;
     float lsum = 0.f;
@@ -257,28 +356,19 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
     for (int db = 0; db < 8; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int tok = t0; tok < t1; tok += 16) {
-      const bool more = tok + 16 < t1;
-      if (more) {
-        const int pg = pg_next >= 0 ? pg_next : page_id(s, tok + 16);
-        wait_lds();  // the stage being refilled was last read one block ago
-        copy_block(tok + 16, pg, stage ^ 1);
-        pg_next = tok + 32 < t1 ? page_id(s, tok + 32) : (has_next ? page_id(sn, wn.t0) : -1);
-        wait_vmem<8>();
-      } else if (has_next) {
-        const int pg = pg_next >= 0 ? pg_next : page_id(sn, wn.t0);
-        wait_lds();  // also: this item's Q has been read
-        copy_q(wn);
-        copy_block(wn.t0, pg, stage ^ 1);
-        pg_next = wn.t0 + 16 < wn.t1 ? page_id(sn, wn.t0 + 16) : -1;
-        wait_vmem<12>();
-      } else {
-        wait_vmem<0>();
-      }
-      const uint32_t st = ring + (uint32_t)(stage * kDecStage);
+      // The workgroup's wavefronts (consecutive kv heads of one share, the
+      // same blocks in the same order) stay in step, so each page is
+      // requested by all of them at once.
+      __builtin_amdgcn_s_barrier();
+      refill();
+      wait_units<U>(issued - consumed - 2);
+      const uint32_t kst = ring + (uint32_t)(r_slot * kDecUnit);
+      const int v_slot = r_slot + 1 == U ? 0 : r_slot + 1;
+      const uint32_t vst = ring + (uint32_t)(v_slot * kDecUnit);
 
       f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sc = mfma16<BF16>(lds_read16(st + k_lds[k]), qf[k], sc);
+      for (int k = 0; k < 4; ++k) sc = mfma16<BF16>(lds_read16(kst + k_lds[k]), qf[k], sc);
 
       float x[4];
       float mx = kNegInf;
@@ -302,14 +392,14 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       m = m_new;
       const u32x2 pf = {pack2<BF16>(x[0], x[1]), pack2<BF16>(x[2], x[3])};
 
-      if (!more && t1 - tok < 16) {
+      if (t1 - tok < 16) {
         // Rows past the item end hold stale cache contents: zero them so that
         // 0 * (stale) can never become NaN.  (16-byte slot q holds part of
         // token row q / 16.)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int q = lane + 64 * u;
-          if ((q >> 4) >= t1 - tok) lds_zero16(st + 4096 + 16 * q);
+          if ((q >> 4) >= t1 - tok) lds_zero16(vst + 16 * q);
         }
       }
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
@@ -318,10 +408,11 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       }
       u32x2 vf[8];
 #pragma unroll
-      for (int db = 0; db < 8; ++db) vf[db] = lds_read_tr16(st + v_lds[db]);
+      for (int db = 0; db < 8; ++db) vf[db] = lds_read_tr16(vst + v_lds[db]);
 #pragma unroll
       for (int db = 0; db < 8; ++db) o[db] = mfma16k16<BF16>(vf[db], pf, o[db]);
-      stage ^= 1;
+      consumed += 2;
+      r_slot = v_slot + 1 == U ? 0 : v_slot + 1;
     }
 
     lsum += xor16(lsum);
@@ -338,17 +429,13 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
         }
         if (a.lse != nullptr && J == 0) a.lse[(size_t)crow * a.hq + chead] = l2 * kLn2;
       } else {
-        const size_t slot = (size_t)(w.part + L / G);
-        float* po = a.part_o + (slot * a.hq + chead) * kHeadDim + 4 * J;
+        const size_t pslot = (size_t)(w.part + L / G);
+        float* po = a.part_o + (pslot * a.hq + chead) * kHeadDim + 4 * J;
 #pragma unroll
         for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db] * inv;
-        if (J == 0) a.part_lse[slot * a.hq + chead] = l2;
+        if (J == 0) a.part_lse[pslot * a.hq + chead] = l2;
       }
     }
-    if (!has_next) break;
-    it = nit;
-    w = wn;
-    s = sn;
   }
 }
 
@@ -625,26 +712,31 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
 // ===========================================================================
 // Split-KV merge
 // ===========================================================================
-// One wavefront per (merged row, head); lane owns 2 of the 128 dims.  The
-// split log-sum-exps are loaded one per lane (nsplit <= 64 per pass) and
-// reduced with wavefront shuffles; the partial rows are then read with up to
-// eight splits in flight.
+// One wavefront per (merged row, head); lane owns 2 of the 128 dims.  Splits
+// are folded in batches of 16 whose log-sum-exps and partial rows are all in
+// flight together.
 template <bool BF16>
 __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
   const int lane = threadIdx.x & 63;
   const int hq = a.hq;
+  const int stride = gridDim.x * 4;
+  int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  // The first row record is requested together with the row count (its
+  // index is clamped into the buffer; it is used only below the count).
+  MergeRow mr = a.rows[min(pair / hq, a.rows_cap - 1)];
   const int n_pairs = uniform(*a.n_rows) * hq;
-  for (int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6); pair < n_pairs; pair += gridDim.x * 4) {
-    const MergeRow mr = a.rows[pair / hq];
+  for (; pair < n_pairs; pair += stride) {
+    if (pair >= stride) mr = a.rows[pair / hq];
     const int h = pair % hq;
-    // Online merge over batches of 8 splits; each batch's log-sum-exps and
-    // partial rows are all requested before any is used.
+    // Online merge over batches of kMergeBatch splits; each batch's
+    // log-sum-exps and partial rows are all requested before any is used.
+    constexpr int kMergeBatch = 16;
     float m = kNegInf, wsum = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int sp0 = 0; sp0 < mr.nsplit; sp0 += 8) {
-      float l[8];
-      float2 v[8];
+    for (int sp0 = 0; sp0 < mr.nsplit; sp0 += kMergeBatch) {
+      float l[kMergeBatch];
+      float2 v[kMergeBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
         const int sp = min(sp0 + u, mr.nsplit - 1);
         const size_t slot = (size_t)(mr.part + sp * mr.stride);
         l[u] = sp0 + u < mr.nsplit ? a.part_lse[slot * hq + h] : kNegInf;
@@ -652,14 +744,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
       }
       float bm = m;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) bm = fmaxf(bm, l[u]);
+      for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, l[u]);
       const float mu = bm == kNegInf ? 0.f : bm;
       const float sc = fast_exp2(m - mu);
       wsum *= sc;
       o0 *= sc;
       o1 *= sc;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
         const float wt = fast_exp2(l[u] - mu);
         wsum += wt;
         o0 += wt * v[u].x;
@@ -677,35 +769,36 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
 // ===========================================================================
 // Launchers
 // ===========================================================================
-#ifndef FEATTN_DECODE_WAVES
-#define FEATTN_DECODE_WAVES 8
-#endif
-constexpr int kDecodeWaves = FEATTN_DECODE_WAVES;
+// Wavefronts per decode workgroup: consecutive kv heads of one share, as
+// many as divide hkv (at most kDecodeWavesPerCu).
+int decode_wg_waves(int hkv) {
+  for (int w = kDecodeWavesPerCu; w > 1; w >>= 1)
+    if (hkv % w == 0) return w;
+  return 1;
+}
 
-int decode_waves() { return kDecodeWaves; }
-
-// Workgroups of the decode kernel that fit one CU at once (160 KB of LDS).
-int decode_wgs_per_cu() { return (int)(163840 / ((size_t)kDecodeWaves * kDecWaveLds)); }
-
-hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st) {
-  (void)nc;  // one MFMA column block serves every decode item (<= 16 columns)
-  const size_t lds = (size_t)kDecodeWaves * kDecWaveLds;
-  static bool lds_ok[2] = {false, false};  // the ring exceeds the 64 KB default
-  if (!lds_ok[bf16]) {
-    hipError_t e = bf16 ? hipFuncSetAttribute((const void*)attn_decode_kernel<true, kDecodeWaves>,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)
-                        : hipFuncSetAttribute((const void*)attn_decode_kernel<false, kDecodeWaves>,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+template <bool BF16, int WAVES>
+static hipError_t decode_launch(const AttnArgs& a, int causal, int grid, hipStream_t st) {
+  const size_t lds = (size_t)WAVES * dec_units<WAVES>() * kDecUnit + 16;
+  static bool lds_ok = false;  // the ring may exceed the 64 KB default
+  if (!lds_ok) {
+    const hipError_t e = hipFuncSetAttribute((const void*)attn_decode_kernel<BF16, WAVES>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    lds_ok[bf16] = true;
+    lds_ok = true;
   }
-  if (bf16)
-    hipLaunchKernelGGL((attn_decode_kernel<true, kDecodeWaves>), dim3(grid), dim3(64 * kDecodeWaves), lds, st, a,
-                       causal);
-  else
-    hipLaunchKernelGGL((attn_decode_kernel<false, kDecodeWaves>), dim3(grid), dim3(64 * kDecodeWaves), lds, st, a,
-                       causal);
+  hipLaunchKernelGGL((attn_decode_kernel<BF16, WAVES>), dim3(grid), dim3(64 * WAVES), lds, st, a, causal);
   return hipGetLastError();
+}
+
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int causal, int grid, hipStream_t st) {
+  switch (waves) {
+    case 8: return bf16 ? decode_launch<true, 8>(a, causal, grid, st) : decode_launch<false, 8>(a, causal, grid, st);
+    case 4: return bf16 ? decode_launch<true, 4>(a, causal, grid, st) : decode_launch<false, 4>(a, causal, grid, st);
+    case 2: return bf16 ? decode_launch<true, 2>(a, causal, grid, st) : decode_launch<false, 2>(a, causal, grid, st);
+    case 1: return bf16 ? decode_launch<true, 1>(a, causal, grid, st) : decode_launch<false, 1>(a, causal, grid, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st) {

@@ -14,6 +14,7 @@ constexpr int kHeadDim = 128;  // the only head size the reference builds (flash
 constexpr int kTileTokens = 64;  // tokens per KV tile of the MFMA tile kernel (4 pages of 16)
 constexpr int kTileCols = 128;   // (q row, head) columns per tile work item (4 waves x 32)
 constexpr int kDecodeCols = 16;  // max (q row, head) columns of one decode work item (one MFMA N block)
+constexpr int kDecodeWavesPerCu = 8;  // decode wavefronts resident per CU (one kv head each)
 
 // Per sequence, derived from the CSR metadata exactly as the reference ATen
 // plan does (portable_gpu_ops.cpp:30): len = (kv[b+1]-kv[b]-1)*page + last[b].
@@ -39,6 +40,38 @@ struct WorkItem {
   int32_t cost;  // planner's cost estimate; unused on the device
 };
 
+// Decode piece as the decode kernel reads it: every query row of sequence
+// `seq` (rows [q0, q0+nq), len tokens, page ids from page_off) against
+// tokens [t0, t1); part as in WorkItem.  Carries the sequence fields itself
+// so that a piece costs one metadata read.
+struct DecodeItem {
+  int32_t q0;
+  int32_t nq;
+  int32_t len;
+  int32_t page_off;
+  int32_t t0;
+  int32_t t1;
+  int32_t part;
+  int32_t seq;
+};
+
+// Start of one decode share (one wavefront per kv head walks it): the range
+// of its pieces in the decode list plus everything the first copies need,
+// so that a wavefront issues its first loads after a single metadata read.
+// pg0 / pg1 are the page ids of the share's first two 16-token blocks (pg1
+// = 0 when there is no second block).  An empty share has it_begin ==
+// it_end.
+struct alignas(64) ShareStart {
+  int32_t it_begin;
+  int32_t it_end;
+  DecodeItem first;
+  int32_t pg0;
+  int32_t pg1;
+  int32_t pad[4];
+};
+static_assert(sizeof(ShareStart) == 64, "one 64-byte scalar load");
+static_assert(sizeof(DecodeItem) == 32, "two pieces per 64 bytes");
+
 // One query row whose tokens were split over `nsplit` work items.  Split s
 // of this row lives in partial slot part + s*stride.
 struct MergeRow {
@@ -59,7 +92,9 @@ struct AttnArgs {
   const int32_t* pages;
   const WorkItem* items;
   const int32_t* n_items;  // device-resident count (graph replays read the current one)
-  const int32_t* share_off;  // decode only: pieces of share k = items[share_off[k] .. share_off[k+1])
+  const DecodeItem* ditems;  // decode only: the pieces, share by share
+  const ShareStart* shares;  // decode only: one record per share
+  int n_share_cap;           // decode only: records in `shares`
   float* part_o;           // [slots][hq][128] fp32, normalised per split
   float* part_lse;         // [slots][hq] log2 domain
   int hq;
@@ -74,6 +109,7 @@ struct MergeArgs {
   float* lse;
   const MergeRow* rows;
   const int32_t* n_rows;
+  int rows_cap;            // entries of `rows`
   const float* part_o;
   const float* part_lse;
   int hq;

@@ -11,6 +11,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
 // ---- element conversions -------------------------------------------------
 // Storage is raw 16-bit; BF16 selects bfloat16 vs IEEE binary16.

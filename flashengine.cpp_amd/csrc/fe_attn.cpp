@@ -20,9 +20,8 @@
 #include "planner.hpp"
 
 namespace feattn {
-hipError_t launch_decode(const AttnArgs& a, bool bf16, int nc, int causal, int grid, hipStream_t st);
-int decode_waves();
-int decode_wgs_per_cu();
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int causal, int grid, hipStream_t st);
+int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
@@ -51,6 +50,9 @@ int hip_fail(hipError_t e, const char* what) {
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Decode share records: one per share the planner may cut (decode_waves / hkv).
+int share_cap(const PlanShape& sh) { return std::max(1, sh.decode_waves / sh.hkv); }
+
 // Offsets of the regions inside the metadata arena (same layout on host and device).
 struct Layout {
   size_t seqs, pages, counts, dshare, decode, tile[2], merge[2], total;
@@ -66,7 +68,7 @@ Layout make_layout(const PlanShape& sh) {
   l.counts = off;
   off = align256(off + sizeof(int32_t) * 8);
   l.dshare = off;
-  off = align256(off + sizeof(int32_t) * ((size_t)sh.decode_waves + 2));
+  off = align256(off + sizeof(ShareStart) * (size_t)share_cap(sh));
   l.decode = off;
   off = align256(off + sizeof(WorkItem) * sh.item_cap);
   for (int m = 0; m < 2; ++m) {
@@ -104,6 +106,7 @@ struct fe_attn_plan {
   bool graph = false;
   int graph_nc = 0;
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
+  int decode_wg = 8;  // wavefronts per decode workgroup
   int decode_nc = 4;
   int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
 };
@@ -139,13 +142,14 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
   sh.num_cus = cus > 0 ? cus : 256;
 
-  sh.decode_waves = sh.num_cus * decode_wgs_per_cu() * decode_waves();
+  sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
   auto* p = new fe_attn_plan();
   p->sh = sh;
   p->bf16 = bf16 != 0;
   p->device = dev;
   p->lay = make_layout(sh);
-  p->grid_decode_cap = sh.num_cus * decode_wgs_per_cu();  // persistent: every workgroup resident
+  p->decode_wg = decode_wg_waves(hkv);
+  p->grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / p->decode_wg;  // persistent: every workgroup resident
   p->grid_tile_cap = sh.num_cus * 2;    // 2 resident 256-thread tile workgroups per CU
   p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head) pairs per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
@@ -211,14 +215,19 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
   if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
   int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
-  const int n_shares = bp.decode_share_off.empty() ? 0 : (int)bp.decode_share_off.size() - 1;
+  const int n_shares = (int)bp.decode_starts.size();
+  const int scap = share_cap(p->sh);
+  if (n_shares > scap) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: decode shares");
   cnt[kCntDecode] = n_shares;
-  std::memcpy(h + l.dshare, bp.decode_share_off.data(), sizeof(int32_t) * bp.decode_share_off.size());
+  // Every record up to the capacity is written: a graph launch covers them
+  // all, and records past the shares in use must read as empty.
+  std::memcpy(h + l.dshare, bp.decode_starts.data(), sizeof(ShareStart) * n_shares);
+  std::memset(h + l.dshare + sizeof(ShareStart) * n_shares, 0, sizeof(ShareStart) * (size_t)(scap - n_shares));
   cnt[kCntTile0] = (int32_t)bp.mode[0].tile.size();
   cnt[kCntTile1] = (int32_t)bp.mode[1].tile.size();
   cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
   cnt[kCntMerge1] = (int32_t)bp.mode[1].merge.size();
-  std::memcpy(h + l.decode, bp.decode.data(), sizeof(WorkItem) * bp.decode.size());
+  std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
   for (int m = 0; m < 2; ++m) {
     std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
     std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
@@ -231,8 +240,8 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e == hipSuccess) e = copy(l.seqs, sizeof(SeqInfo) * bp.seqs.size());
   if (e == hipSuccess) e = copy(l.pages, sizeof(int32_t) * npages);
   if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
-  if (e == hipSuccess) e = copy(l.dshare, sizeof(int32_t) * bp.decode_share_off.size());
-  if (e == hipSuccess) e = copy(l.decode, sizeof(WorkItem) * bp.decode.size());
+  if (e == hipSuccess) e = copy(l.dshare, sizeof(ShareStart) * (size_t)scap);
+  if (e == hipSuccess) e = copy(l.decode, sizeof(DecodeItem) * bp.decode_items.size());
   for (int m = 0; m < 2 && e == hipSuccess; ++m) {
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
     if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
@@ -281,12 +290,13 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
   hipError_t e;
   if (p->graph || p->n_decode > 0) {
     AttnArgs d = a;
-    d.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.decode);
-    d.share_off = reinterpret_cast<const int32_t*>(p->dev + p->lay.dshare);
+    d.ditems = reinterpret_cast<const DecodeItem*>(p->dev + p->lay.decode);
+    d.shares = reinterpret_cast<const ShareStart*>(p->dev + p->lay.dshare);
+    d.n_share_cap = share_cap(p->sh);
     d.n_items = counts + kCntDecode;
-    const int wv = decode_waves();
+    const int wv = p->decode_wg;
     const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + wv - 1) / wv);
-    e = launch_decode(d, p->bf16, p->decode_nc, causal ? 1 : 0, std::max(grid, 1), st);
+    e = launch_decode(d, p->bf16, p->decode_wg, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
   if (p->graph || p->n_tile[mode] > 0) {
@@ -303,6 +313,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     m.lse = lse;
     m.rows = reinterpret_cast<const MergeRow*>(p->dev + p->lay.merge[mode]);
     m.n_rows = counts + (mode ? kCntMerge1 : kCntMerge0);
+    m.rows_cap = p->sh.partial_cap;
     m.part_o = p->part_o;
     m.part_lse = p->part_lse;
     m.hq = p->sh.hq;

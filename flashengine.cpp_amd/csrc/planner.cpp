@@ -21,6 +21,15 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Share boundaries (token offsets into the decode stream, multiples of 16):
+// equal shares of `quota` tokens.
+std::vector<int64_t> cut_uniform(int64_t stream, int64_t quota) {
+  std::vector<int64_t> cuts;
+  for (int64_t c = 0; c < stream; c += quota) cuts.push_back(c);
+  cuts.push_back(stream);
+  return cuts;
+}
+
 // Sorts by decreasing cost so the longest items start first (LPT order).
 void order_items(std::vector<WorkItem>& items) {
   std::stable_sort(items.begin(), items.end(),
@@ -139,54 +148,94 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
     }
   }
   out.decode_nc = max_cols <= 4 ? 4 : max_cols <= 8 ? 8 : 16;
-  const int shares = std::max(1, sh.decode_waves / sh.hkv);
+  const int n_static = std::max(1, sh.decode_waves / sh.hkv);
   if (stream > 0) {
-    int64_t quota = std::max<int64_t>(kMinShareTokens, round_up((int)((stream + shares - 1) / shares), 16));
-    for (;;) {
-      // partial slots needed with this quota
-      int64_t slots = 0, pieces = 0, off = 0;
+    // Partial slots and pieces that a cut needs (a sequence overlapping
+    // several shares is cut into pieces, each with qlen partial rows).
+    auto cost_of = [&](const std::vector<int64_t>& cuts, int64_t& slots, int64_t& pieces) {
+      slots = pieces = 0;
+      int64_t off = 0;
+      size_t k = 0;
       for (int b = 0; b < batch; ++b) {
         const SeqInfo& s = out.seqs[b];
         if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
         const int64_t end = off + round_up(s.len, 16);
-        const int64_t np = (end - 1) / quota - off / quota + 1;
+        while (cuts[k + 1] <= off) ++k;
+        size_t k1 = k;
+        while (cuts[k1 + 1] < end) ++k1;
+        const int64_t np = (int64_t)(k1 - k + 1);
         if (np > 1) slots += np * s.qlen;
         pieces += np;
         off = end;
       }
-      if (slots <= slot_budget && pieces <= sh.item_cap) break;
+    };
+    auto fits = [&](const std::vector<int64_t>& cuts) {
+      int64_t slots, pieces;
+      cost_of(cuts, slots, pieces);
+      return slots <= slot_budget && pieces <= sh.item_cap;
+    };
+    std::vector<int64_t> cuts;
+    int64_t quota = std::max<int64_t>(kMinShareTokens, round_up((int)((stream + n_static - 1) / n_static), 16));
+    for (;;) {
+      cuts = cut_uniform(stream, quota);
+      if (fits(cuts)) break;
       if (quota >= stream) {
         err = "attention metadata exceeds capacity: decode work list";
         return FE_ECAPACITY;
       }
       quota *= 2;
     }
-    const int used = (int)((stream + quota - 1) / quota);
+    const int used = (int)cuts.size() - 1;
     out.decode_share_off.assign(used + 1, 0);
     int64_t off = 0;
     int share = 0;
+    size_t k = 0;
     for (int b = 0; b < batch; ++b) {
       const SeqInfo& s = out.seqs[b];
       if (s.qlen == 0 || s.qlen * G > kDecodeCols) continue;
       const int64_t end = off + round_up(s.len, 16);
-      const int k0 = (int)(off / quota), k1 = (int)((end - 1) / quota);
-      const int np = k1 - k0 + 1;
+      while (cuts[k + 1] <= off) ++k;
+      size_t k1 = k;
+      while (cuts[k1 + 1] < end) ++k1;
+      const int np = (int)(k1 - k + 1);
       int base = -1;
       if (np > 1) {
         base = out.decode_partials;
         out.decode_partials += np * s.qlen;
         for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, np, s.qlen});
       }
-      for (int k = k0; k <= k1; ++k) {
-        while (share < k) out.decode_share_off[++share] = (int32_t)out.decode.size();
-        const int t0 = (int)(std::max<int64_t>(off, (int64_t)k * quota) - off);
-        const int t1 = (int)std::min<int64_t>(s.len, std::min<int64_t>(end, (int64_t)(k + 1) * quota) - off);
+      for (size_t j = k; j <= k1; ++j) {
+        while (share < (int)j) out.decode_share_off[++share] = (int32_t)out.decode.size();
+        const int t0 = (int)(std::max<int64_t>(off, cuts[j]) - off);
+        const int t1 = (int)std::min<int64_t>(s.len, std::min<int64_t>(end, cuts[j + 1]) - off);
         out.decode.push_back(
-            WorkItem{b, s.qo, s.qlen, 0, t0, t1, base < 0 ? -1 : base + (k - k0) * s.qlen, t1 - t0});
+            WorkItem{b, s.qo, s.qlen, 0, t0, t1, base < 0 ? -1 : base + (int)(j - k) * s.qlen, t1 - t0});
       }
       off = end;
     }
     while (share < used) out.decode_share_off[++share] = (int32_t)out.decode.size();
+    out.decode_items.resize(out.decode.size());
+    for (size_t i = 0; i < out.decode.size(); ++i) {
+      const WorkItem& w = out.decode[i];
+      const SeqInfo& sq = out.seqs[w.seq];
+      out.decode_items[i] = DecodeItem{w.q0, w.nq, sq.len, sq.page_off, w.t0, w.t1, w.part, w.seq};
+    }
+    auto page_of = [&](const DecodeItem& d, int tok) { return pages[d.page_off + tok / sh.page]; };
+    out.decode_starts.assign(used, ShareStart{});
+    for (int k = 0; k < used; ++k) {
+      ShareStart& ss = out.decode_starts[k];
+      ss.it_begin = out.decode_share_off[k];
+      ss.it_end = out.decode_share_off[k + 1];
+      if (ss.it_begin >= ss.it_end) continue;
+      const DecodeItem& d = out.decode_items[ss.it_begin];
+      ss.first = d;
+      ss.pg0 = page_of(d, d.t0);
+      if (d.t0 + 16 < d.t1) ss.pg1 = page_of(d, d.t0 + 16);
+      else if (ss.it_begin + 1 < ss.it_end) {
+        const DecodeItem& d2 = out.decode_items[ss.it_begin + 1];
+        ss.pg1 = page_of(d2, d2.t0);
+      }
+    }
   }
 
   // ---- tile items, per mask mode.

@@ -35,6 +35,8 @@ struct BuiltPlan {
   std::vector<SeqInfo> seqs;
   std::vector<WorkItem> decode;  // decode pieces (kvh unset), identical for both masks
   std::vector<int32_t> decode_share_off;  // CSR: pieces of share k = [off[k], off[k+1])
+  std::vector<DecodeItem> decode_items;   // `decode` in the decode kernel's format
+  std::vector<ShareStart> decode_starts;  // one per share in use
   int decode_partials = 0;
   std::vector<MergeRow> decode_merge;
   int decode_nc = 4;             // 4, 8 or 16 columns per decode item
