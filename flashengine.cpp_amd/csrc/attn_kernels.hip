@@ -379,9 +379,12 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       }
       mx = fmaxf(mx, xor16(mx));
       mx = fmaxf(mx, xor32(mx));
-      const float m_new = fmaxf(m, mx);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = fast_exp2(m - m_use);
+      // Lazy reference maximum: raised (with l and o rescaled) only when the
+      // block maximum exceeds it by more than 8, so p <= 2^8.
+      const bool up = mx > m + 8.f;
+      const float alpha = up ? fast_exp2(m - mx) : 1.f;
+      if (up) m = mx;
+      const float m_use = m == kNegInf ? 0.f : m;
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -389,7 +392,6 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
         ps += x[r];
       }
       lsum = lsum * alpha + ps;
-      m = m_new;
       const u32x2 pf = {pack2<BF16>(x[0], x[1]), pack2<BF16>(x[2], x[3])};
 
       if (t1 - tok < 16) {
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
           if ((q >> 4) >= t1 - tok) lds_zero16(vst + 16 * q);
         }
       }
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+      if (__builtin_amdgcn_ballot_w64(up) != 0) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[db] *= alpha;
       }
@@ -574,9 +576,13 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
         }
       mx = fmaxf(mx, xor16(mx));
       mx = fmaxf(mx, xor32(mx));
-      const float m_new = fmaxf(m[cb], mx * a.scale_log2);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = fast_exp2(m[cb] - m_use);
+      // Lazy reference maximum: raised (with l and o rescaled) only when the
+      // tile maximum exceeds it by more than 8, so p <= 2^8.
+      const float mt = mx * a.scale_log2;
+      const bool up = mt > m[cb] + 8.f;
+      const float alpha = up ? fast_exp2(m[cb] - mt) : 1.f;
+      if (up) m[cb] = mt;
+      const float m_use = m[cb] == kNegInf ? 0.f : m[cb];
       float x[4][4];
       float ps = 0.f;
 #pragma unroll
@@ -587,8 +593,7 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
           ps += x[tb][r];
         }
       lsum[cb] = lsum[cb] * alpha + ps;
-      m[cb] = m_new;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+      if (__builtin_amdgcn_ballot_w64(up) != 0) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[db][cb] *= alpha;
       }

@@ -57,14 +57,15 @@ __device__ __forceinline__ uint32_t from_f32_rne(float f) {
 // identity, is the contract.
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  // one v_cvt_pk_{bf16,f16}_f32 (round to nearest even) for both halves
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {a, b};
   if constexpr (BF16) {
-    uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)a);
-    uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)b);
-    return lo | (hi << 16);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   } else {
-    uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
-    uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
-    return lo | (hi << 16);
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
   }
 }
 
