@@ -471,15 +471,37 @@ struct TileLanes {
   uint32_t k_lds[4], v_lds[8];
 };
 
+// Copies this wavefront's 16-token block (tokens T + 16 wave ..) of item
+// w's tile starting at token T into ring stage `stage`; blocks at or past the
+// item end are skipped.
+__device__ __forceinline__ void tile_copy(const AttnArgs& a, const WorkItem& w, const SeqInfo& s,
+                                          const TileLanes& tl, uint32_t lbase, int wave, int T, int stage) {
+  const int tok = T + 16 * wave;
+  if (tok >= w.t1) return;
+  const int pshift = a.page_shift;
+  const int row_bytes = a.hkv * kHeadDim * 2;
+  const int pg = ldc(a.pages, s.page_off + (tok >> pshift));
+  const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & ((1 << pshift) - 1))) * (size_t)row_bytes +
+                     (size_t)w.kvh * kHeadDim * 2;
+  const char* kb = reinterpret_cast<const char*>(a.kc) + blk;
+  const char* vb = reinterpret_cast<const char*>(a.vc) + blk;
+  const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) lds_dma16(kb + tl.k_goff[r], st + wave * kTileBlock + 1024 * r);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) lds_dma16(vb + tl.v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
+}
+
+// Computes item w whose first tile was already requested into stage
+// `stage0`; during its last tile the first tile of the next item (wn, sn) is
+// requested into the other stage, whose index is returned.
 template <bool BF16, bool CAUSAL, int NCB>
-__device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, const SeqInfo& s,
-                                          const TileLanes& tl, uint32_t lbase, int wave, int lane) {
+__device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, const SeqInfo& s, bool has_next,
+                                         const WorkItem& wn, const SeqInfo& sn, const TileLanes& tl, uint32_t lbase,
+                                         int wave, int lane, int stage0) {
   const int J = lane >> 4;
   const int L = lane & 15;
   const int G = a.group;
-  const int pshift = a.page_shift;
-  const int pmask = (1 << pshift) - 1;
-  const int row_bytes = a.hkv * kHeadDim * 2;
   const int kvh = w.kvh;
   const int t0 = w.t0;
   const int t1 = w.t1;
@@ -487,23 +509,6 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
   constexpr int kWcols = 16 * NCB;  // columns per wavefront
   const bool wave_on = wave * kWcols < ncols;
 
-  // This wavefront's block of a tile: K and V rows [T + 16 wave, +16).
-  const char* kb0 = reinterpret_cast<const char*>(a.kc) + (size_t)kvh * kHeadDim * 2;
-  const char* vb0 = reinterpret_cast<const char*>(a.vc) + (size_t)kvh * kHeadDim * 2;
-  auto copy_block = [&](int T, int stage) {
-    const int tok = T + 16 * wave;
-    if (tok >= t1) return;
-    const int pg = ldc(a.pages, s.page_off + (tok >> pshift));
-    const size_t blk = (((size_t)pg << pshift) + (size_t)(tok & pmask)) * (size_t)row_bytes;
-    const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lds_dma16(kb0 + blk + tl.k_goff[r], st + wave * kTileBlock + 1024 * r);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lds_dma16(vb0 + blk + tl.v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
-  };
-
-  wait_lds();
-  copy_block(t0, 0);
 
   int lim[NCB], crow[NCB], chead[NCB];
   u32x4 qf[NCB][4];
@@ -619,7 +624,7 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
       }
   };
 
-  int stage = 0;
+  int stage = stage0;
   for (int T = t0; T < t1; T += kTileTokens) {
     wait_vmem<0>();  // this wavefront's block of the tile has landed
     const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
@@ -636,7 +641,8 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
       }
     }
     __syncthreads();  // every block of the tile is in LDS; the other stage is free
-    if (T + kTileTokens < t1) copy_block(T + kTileTokens, stage ^ 1);
+    if (T + kTileTokens < t1) tile_copy(a, w, s, tl, lbase, wave, T + kTileTokens, stage ^ 1);
+    else if (has_next) tile_copy(a, wn, sn, tl, lbase, wave, wn.t0, stage ^ 1);
     if (wave_on) {
       if (T + kTileTokens - 1 <= lim_min) compute(st, T, std::false_type{});
       else compute(st, T, std::true_type{});
@@ -673,6 +679,7 @@ __device__ __forceinline__ void tile_item(const AttnArgs& a, const WorkItem& w, 
       }
     }
   }
+  return stage;
 }
 
 template <bool BF16, bool CAUSAL>
@@ -705,12 +712,29 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
     }
   }
 
-  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const WorkItem w = ldc_item(a.items, it);
-    const SeqInfo s = ldc_seq(a.seqs, w.seq);
-    if (w.nq * a.group <= 64) tile_item<BF16, CAUSAL, 1>(a, w, s, tl, lbase, wave, lane);
-    else tile_item<BF16, CAUSAL, 2>(a, w, s, tl, lbase, wave, lane);
-    __syncthreads();  // the ring is reused by the next item
+  // Items it, it + gridDim.x, ...; each item's first tile is requested
+  // during the previous item's last tile.
+  int it = blockIdx.x;
+  if (it >= n_items) return;
+  WorkItem w = ldc_item(a.items, it);
+  SeqInfo s = ldc_seq(a.seqs, w.seq);
+  tile_copy(a, w, s, tl, lbase, wave, w.t0, 0);
+  int stage = 0;
+  for (;;) {
+    const int nit = it + gridDim.x;
+    const bool has_next = nit < n_items;
+    WorkItem wn = w;
+    SeqInfo sn = s;
+    if (has_next) {
+      wn = ldc_item(a.items, nit);
+      sn = ldc_seq(a.seqs, wn.seq);
+    }
+    if (w.nq * a.group <= 64) stage = tile_item<BF16, CAUSAL, 1>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
+    else stage = tile_item<BF16, CAUSAL, 2>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
+    if (!has_next) break;
+    it = nit;
+    w = wn;
+    s = sn;
   }
 }
 
