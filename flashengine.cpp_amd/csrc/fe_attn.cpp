@@ -9,6 +9,7 @@
 // the plan capacity in graph mode, so a captured graph stays valid across
 // prepares.
 #include "fe_attn.h"
+#include "fe_driver.h"
 
 #include <hip/hip_runtime.h>
 
@@ -28,6 +29,7 @@ hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache,
                        bool bf16, int max_pos, hipStream_t st);
 hipError_t launch_store(const void* k, const void* v, void* kc, void* vc, const int64_t* slots, int rows, int width,
                         int64_t cache_slots, hipStream_t st);
+hipError_t launch_rope_table(float* table, int max_len, int dim, float theta, hipStream_t st);
 hipError_t launch_rope_append(void* q, const void* k, const void* v, void* kc, void* vc, const int64_t* pos,
                               const int64_t* slots, const float* cache, int rows, int hq, int hkv, int dim, bool bf16,
                               int max_pos, int64_t cache_slots, hipStream_t st);
@@ -89,6 +91,12 @@ enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 
 constexpr size_t kPartialBytes = 64u << 20;  // split-KV workspace (fp32 partial rows)
 
 }  // namespace
+
+namespace feattn {
+// Shared with the host driver (driver.cpp): sets the message returned by
+// fe_attn_last_error() on this thread and returns `code`.
+int report_error(int code, const std::string& msg) { return fail(code, msg); }
+}  // namespace feattn
 
 struct fe_attn_plan {
   PlanShape sh;
@@ -323,6 +331,16 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
   }
   return FE_OK;
+}
+
+int fe_rope_table(float* table, int max_len, int dim, double theta, void* stream) {
+  if (table == nullptr) return fail(FE_EINVAL, "rope table: null pointer");
+  if (max_len <= 0 || dim <= 0 || dim % 2 != 0) return fail(FE_EINVAL, "rope table: max_len > 0 and even dim required");
+  if (!(theta > 0.0)) return fail(FE_EINVAL, "rope table: theta must be positive");
+  if ((int64_t)max_len * (dim / 2) > (int64_t)INT32_MAX * 128)
+    return fail(FE_EINVAL, "rope table: max_len * dim / 2 exceeds the launch range");
+  const hipError_t e = launch_rope_table(table, max_len, dim, (float)theta, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "rope table kernel launch");
 }
 
 int fe_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim, int bf16,

@@ -214,4 +214,26 @@ hipError_t launch_rope_append(void* q, const void* k, const void* v, void* kc, v
   return hipGetLastError();
 }
 
+// RoPE table (reference src/cuda_model.cpp:44-47), one thread per (position,
+// frequency): inv = 1 / theta^((2i)/dim), f = p * inv in fp32 (this file is
+// compiled without FMA contraction), cos | sin halves.
+__global__ void rope_table_kernel(float* table, int max_len, int dim, float theta) {
+  const int half = dim / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)max_len * half) return;
+  const int p = (int)(idx / half);
+  const int i = (int)(idx % half);
+  const float inv = 1.0f / powf(theta, (float)(2 * i) / (float)dim);
+  const float f = (float)p * inv;
+  table[(size_t)p * dim + i] = cosf(f);
+  table[(size_t)p * dim + half + i] = sinf(f);
+}
+
+hipError_t launch_rope_table(float* table, int max_len, int dim, float theta, hipStream_t st) {
+  const int64_t n = (int64_t)max_len * (dim / 2);
+  const int grid = (int)((n + 255) / 256);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(grid), dim3(256), 0, st, table, max_len, dim, theta);
+  return hipGetLastError();
+}
+
 }  // namespace feattn

@@ -41,6 +41,19 @@ C_SYMBOLS = (
     "fe_attn_version",
 )
 
+# Every extern "C" symbol of include/fe_driver.h.
+DRIVER_SYMBOLS = (
+    "fe_graph_buckets",
+    "fe_blocks_create",
+    "fe_blocks_destroy",
+    "fe_blocks_ensure",
+    "fe_blocks_release",
+    "fe_blocks_table",
+    "fe_blocks_used",
+    "fe_prepare_metadata",
+    "fe_rope_table",
+)
+
 _LIB: Optional[ctypes.CDLL] = None
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -78,6 +91,21 @@ def lib() -> ctypes.CDLL:
     for name in C_SYMBOLS:
         getattr(L, name).restype = ctypes.c_char_p if name in (
             "fe_attn_last_error", "fe_attn_version") else _int
+    _i64 = ctypes.c_int64
+    _i64p = ctypes.POINTER(ctypes.c_int64)
+    L.fe_graph_buckets.argtypes = [_i64, _i64p, _int, ctypes.POINTER(_int)]
+    L.fe_blocks_create.argtypes = [_i64, _i64, ctypes.POINTER(_vp)]
+    L.fe_blocks_destroy.argtypes = [_vp]
+    L.fe_blocks_ensure.argtypes = [_vp, _i64, _i64, ctypes.POINTER(_int)]
+    L.fe_blocks_release.argtypes = [_vp, _i64]
+    L.fe_blocks_table.argtypes = [_vp, _i64, _i32p, _int, ctypes.POINTER(_int)]
+    L.fe_blocks_used.argtypes = [_vp]
+    L.fe_prepare_metadata.argtypes = ([_int, _i64p, _i32p, _i32p, _i32p, _int, _int, _int, _i64, ctypes.c_int32,
+                                       _i64p, _i64p, _int, _i32p, _i32p, _i32p, _int, _i32p,
+                                       ctypes.POINTER(_int), ctypes.POINTER(_int)])
+    L.fe_rope_table.argtypes = [_vp, _int, _int, ctypes.c_double, _vp]
+    for name in DRIVER_SYMBOLS:
+        getattr(L, name).restype = _i64 if name == "fe_blocks_used" else _int
     _LIB = L
     return L
 
@@ -192,3 +220,95 @@ def dump(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, last, 
 
 def version() -> str:
     return lib().fe_attn_version().decode()
+
+
+# ---------------------------------------------------------------------------
+# Host driver (include/fe_driver.h)
+# ---------------------------------------------------------------------------
+
+def graph_buckets(maximum: int):
+    """fe::graph_buckets (src/common.cpp:45-51): batch sizes that get a graph."""
+    n = _int()
+    _check(lib().fe_graph_buckets(maximum, None, 0, ctypes.byref(n)))
+    out = (ctypes.c_int64 * max(1, n.value))()
+    _check(lib().fe_graph_buckets(maximum, out, n.value, ctypes.byref(n)))
+    return list(out[:n.value])
+
+
+class Blocks:
+    """FIFO KV page allocator: the page-table side of fe::BlockManager
+    (src/scheduler.cpp:5,31-35), sequences keyed by an integer id."""
+
+    def __init__(self, total: int, block_size: int):
+        handle = _vp()
+        _check(lib().fe_blocks_create(total, block_size, ctypes.byref(handle)))
+        self._h = handle
+
+    def ensure(self, seq: int, target_tokens: int) -> bool:
+        ok = _int()
+        _check(lib().fe_blocks_ensure(self._h, seq, target_tokens, ctypes.byref(ok)))
+        return bool(ok.value)
+
+    def release(self, seq: int) -> None:
+        _check(lib().fe_blocks_release(self._h, seq))
+
+    def table(self, seq: int):
+        n = _int()
+        _check(lib().fe_blocks_table(self._h, seq, None, 0, ctypes.byref(n)))
+        out = (ctypes.c_int32 * max(1, n.value))()
+        _check(lib().fe_blocks_table(self._h, seq, out, n.value, ctypes.byref(n)))
+        return list(out[:n.value])
+
+    def used(self) -> int:
+        return lib().fe_blocks_used(self._h)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().fe_blocks_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def prepare_metadata(starts, rows, tables, page: int, max_model_len: int, count: Optional[int] = None,
+                     entry_rows: int = 0, dummy_page: int = 0):
+    """CudaModel::prepare (src/cuda_model.cpp:131-142): returns a dict of numpy
+    arrays positions, slots (int64) and qo, kv, pages, last (int32)."""
+    import numpy as np
+
+    n = len(starts)
+    count = n if count is None else count
+    off = [0]
+    for t in tables:
+        off.append(off[-1] + len(t))
+    flat = [p for t in tables for p in t]
+    c_start = (ctypes.c_int64 * max(1, n))(*starts)
+    c_rows = _i32(rows)
+    c_off = _i32(off)
+    c_tab = _i32(flat)
+    nr, npg = _int(), _int()
+    args = (n, c_start, c_rows, c_off, c_tab, count, entry_rows, page, max_model_len, dummy_page)
+    _check(lib().fe_prepare_metadata(*args, None, None, 0, None, None, None, 0, None, ctypes.byref(nr),
+                                     ctypes.byref(npg)))
+    positions = np.zeros(max(1, nr.value), np.int64)
+    slots = np.zeros(max(1, nr.value), np.int64)
+    qo = np.zeros(count + 1, np.int32)
+    kv = np.zeros(count + 1, np.int32)
+    pages = np.zeros(max(1, npg.value), np.int32)
+    last = np.zeros(max(1, count), np.int32)
+    p64 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+    p32 = lambda a: a.ctypes.data_as(_i32p)
+    _check(lib().fe_prepare_metadata(*args, p64(positions), p64(slots), nr.value, p32(qo), p32(kv), p32(pages),
+                                     npg.value, p32(last), ctypes.byref(nr), ctypes.byref(npg)))
+    return {"positions": positions[:nr.value], "slots": slots[:nr.value], "qo": qo, "kv": kv,
+            "pages": pages[:npg.value], "last": last[:count]}
+
+
+def rope_table(table, max_len: int, dim: int, theta: float, stream=None) -> None:
+    """Fills a device fp32 tensor [max_len, dim] with the cos | sin table
+    (src/cuda_model.cpp:44-47)."""
+    _check(lib().fe_rope_table(_ptr(table), max_len, dim, float(theta), _stream(stream)))

@@ -17,15 +17,22 @@ def header_functions(path):
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fe_\w+)\s*\(", text, flags=re.M)))
 
 
+HEADERS = {"fe_attn.h": feattn.C_SYMBOLS, "fe_driver.h": feattn.DRIVER_SYMBOLS}
+
+
 def test_header_matches_binding_list():
-    names = header_functions(os.path.join(ROOT, "include", "fe_attn.h"))
-    assert names == sorted(feattn.C_SYMBOLS)
+    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == sorted(
+        list(HEADERS) + ["fe_native_hip.hpp"])
+    for header, symbols in HEADERS.items():
+        names = header_functions(os.path.join(ROOT, "include", header))
+        assert names == sorted(symbols), header
 
 
 def test_library_exports_every_c_symbol():
     lib = feattn.lib()
-    for name in header_functions(os.path.join(ROOT, "include", "fe_attn.h")):
-        assert hasattr(lib, name), name
+    for header in HEADERS:
+        for name in header_functions(os.path.join(ROOT, "include", header)):
+            assert hasattr(lib, name), name
     assert feattn.version().startswith("feattn-hip-gfx950")
 
 
