@@ -161,13 +161,23 @@ def _prefill(b, dev, res):
     ra = lambda i: feattn.rope_append(q, k, v, kc, vc, pos, slots, table, b.rows, b.hq, b.hkv, 128,
                                       True, 8192, b.cache_slots)
     ms_ra = event_time_ms(ra, 20, 3)
+    # the same new tokens through the fused q/k RMSNorm + RoPE + append of a
+    # [rows][q | k | v] projection (src/cuda_model.cpp:91-95 in one pass)
+    qkv = torch.randn(b.rows, (b.hq + 2 * b.hkv) * 128, device=dev).to(torch.bfloat16)
+    qw = torch.ones(128, device=dev, dtype=torch.bfloat16)
+    q_out = torch.empty_like(q)
+    nra = lambda i: feattn.norm_rope_append(qkv, qkv.shape[1], qw, qw, 1e-6, q_out, kc, vc, pos, slots, table,
+                                            b.rows, b.hq, b.hkv, True, 8192, b.cache_slots)
+    ms_nra = event_time_ms(nra, 20, 3)
     res["prefill_qwen3_8b"] = {
         "workload": "8 seqs, prefix U[0,2048], chunks >=64 summing to 8192, causal, bf16",
         "attn_ms": round(ms, 4), "attn_tflops": round(flops / ms / 1e9, 2),
         "attn_frac_of_bf16_peak": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
         "gflop": round(flops / 1e9, 2),
         "rope_append_ms": round(ms_ra, 4),
-        "rope_append_gbs": round(W.rope_append_bytes(b) / ms_ra / 1e6, 1)}
+        "rope_append_gbs": round(W.rope_append_bytes(b) / ms_ra / 1e6, 1),
+        "norm_rope_append_ms": round(ms_nra, 4),
+        "norm_rope_append_gbs": round(W.norm_rope_append_bytes(b) / ms_nra / 1e6, 1)}
     log("prefill", res["prefill_qwen3_8b"])
 
 

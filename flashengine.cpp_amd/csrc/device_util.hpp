@@ -39,7 +39,11 @@ __device__ __forceinline__ float hi_f32(uint32_t w) {
 
 // fp32 -> 16-bit, round to nearest even.  The bf16 path is written out in
 // integer arithmetic so it is the same function as ATen's CPU conversion
-// (NaN -> 0x7fc0); the fp16 path is the hardware RNE conversion.
+// (NaN -> 0x7fc0); the fp16 path is the hardware RNE conversion of the
+// already-rounded fp32 value.  The empty asm pins that value in a register:
+// otherwise the backend may fold a preceding multiply into the conversion
+// (v_fma_mixlo_f16), which rounds the exact product straight to fp16 and
+// differs from rounding to fp32 first whenever the fp32 product is a tie.
 template <bool BF16>
 __device__ __forceinline__ uint32_t from_f32_rne(float f) {
   if constexpr (BF16) {
@@ -48,6 +52,7 @@ __device__ __forceinline__ uint32_t from_f32_rne(float f) {
     u += 0x7fffu + ((u >> 16) & 1u);
     return u >> 16;
   } else {
+    asm("" : "+v"(f));
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
   }
 }

@@ -10,6 +10,7 @@
 // prepares.
 #include "fe_attn.h"
 #include "fe_driver.h"
+#include "fe_ops.h"
 
 #include <hip/hip_runtime.h>
 
@@ -30,6 +31,15 @@ hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache,
 hipError_t launch_store(const void* k, const void* v, void* kc, void* vc, const int64_t* slots, int rows, int width,
                         int64_t cache_slots, hipStream_t st);
 hipError_t launch_rope_table(float* table, int max_len, int dim, float theta, hipStream_t st);
+hipError_t launch_norm(const void* x, const void* res, const void* w, void* out, void* new_res, int rows, int width,
+                       float eps, bool bf16, hipStream_t st);
+hipError_t launch_norm_rope_append(const void* qkv, int64_t row_stride, const void* qw, const void* kw, float eps,
+                                   void* q_out, void* kc, void* vc, const int64_t* pos, const int64_t* slots,
+                                   const float* cache, int rows, int hq, int hkv, bool bf16, int max_pos,
+                                   int64_t cache_slots, hipStream_t st);
+hipError_t launch_silu_mul(const void* gu, void* out, int rows, int width, bool bf16, hipStream_t st);
+hipError_t launch_accept(const int64_t* draft, const int64_t* verify, int64_t* out, int batch, int k,
+                         hipStream_t st);
 hipError_t launch_rope_append(void* q, const void* k, const void* v, void* kc, void* vc, const int64_t* pos,
                               const int64_t* slots, const float* cache, int rows, int hq, int hkv, int dim, bool bf16,
                               int max_pos, int64_t cache_slots, hipStream_t st);
@@ -380,6 +390,54 @@ int fe_rope_append(void* q, const void* k, const void* v, void* k_cache, void* v
   const hipError_t e = launch_rope_append(q, k, v, k_cache, v_cache, pos, slots, cache, rows, hq, hkv, dim,
                                           bf16 != 0, max_positions, cache_slots, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FE_OK : hip_fail(e, "rope_append kernel launch");
+}
+
+int fe_norm(const void* x, const void* residual, const void* weight, void* output, void* new_residual, int rows,
+            int width, float eps, int bf16, void* stream) {
+  if (rows < 0 || width <= 0) return fail(FE_EINVAL, "norm: rows >= 0 and width > 0 required");
+  if (rows == 0) return FE_OK;
+  if (x == nullptr || weight == nullptr || output == nullptr) return fail(FE_EINVAL, "norm: null pointer");
+  const hipError_t e = launch_norm(x, residual, weight, output, new_residual, rows, width, eps, bf16 != 0,
+                                   static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "norm kernel launch");
+}
+
+int fe_silu_mul(const void* gate_up, void* output, int rows, int width, int bf16, void* stream) {
+  if (rows < 0 || width < 0) return fail(FE_EINVAL, "silu_mul: negative size");
+  if ((int64_t)rows * width == 0) return FE_OK;
+  if (gate_up == nullptr || output == nullptr) return fail(FE_EINVAL, "silu_mul: null pointer");
+  const hipError_t e = launch_silu_mul(gate_up, output, rows, width, bf16 != 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "silu_mul kernel launch");
+}
+
+int fe_accept(const int64_t* draft, const int64_t* verify, int64_t* out, int batch, int k, void* stream) {
+  if (batch < 0 || k < 0) return fail(FE_EINVAL, "accept: negative size");
+  if (batch == 0) return FE_OK;
+  if (draft == nullptr || verify == nullptr || out == nullptr) return fail(FE_EINVAL, "accept: null pointer");
+  const hipError_t e = launch_accept(draft, verify, out, batch, k, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "accept kernel launch");
+}
+
+int fe_norm_rope_append(const void* qkv, int64_t row_stride, const void* q_weight, const void* k_weight, float eps,
+                        void* q_out, void* k_cache, void* v_cache, const int64_t* pos, const int64_t* slots,
+                        const float* cache, int rows, int hq, int hkv, int dim, int bf16, int max_positions,
+                        int cache_slots, void* stream) {
+  if (rows < 0 || hq < 0 || hkv < 0 || cache_slots < 0) return fail(FE_EINVAL, "norm_rope_append: negative size");
+  if (dim != kHeadDim) return fail(FE_EINVAL, "norm_rope_append: head dim must be 128");
+  if (rows == 0 || hq + hkv == 0) return FE_OK;
+  if (row_stride < (int64_t)(hq + 2 * hkv) * dim || row_stride % 8 != 0)
+    return fail(FE_EINVAL, "norm_rope_append: row_stride must cover hq + 2*hkv heads and be a multiple of 8");
+  if (qkv == nullptr || pos == nullptr || cache == nullptr || (hq > 0 && (q_out == nullptr || q_weight == nullptr)) ||
+      (hkv > 0 && (k_weight == nullptr || k_cache == nullptr || v_cache == nullptr || slots == nullptr)))
+    return fail(FE_EINVAL, "norm_rope_append: null pointer");
+  const void* ptrs[] = {qkv, q_weight, k_weight, q_out, k_cache, v_cache};
+  for (const void* ptr : ptrs)
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+      return fail(FE_EINVAL, "norm_rope_append: tensors must be 16-byte aligned");
+  const hipError_t e = launch_norm_rope_append(qkv, row_stride, q_weight, k_weight, eps, q_out, k_cache, v_cache, pos,
+                                               slots, cache, rows, hq, hkv, bf16 != 0, max_positions, cache_slots,
+                                               static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FE_OK : hip_fail(e, "norm_rope_append kernel launch");
 }
 
 int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks,

@@ -5,6 +5,7 @@
 #include <string>
 
 #include "fe_attn.h"
+#include "fe_ops.h"
 #include "fe_native_hip.hpp"
 
 namespace fe::cuda {
@@ -45,6 +46,27 @@ void attention_lse(AttentionPlan* plan, void* q, void* k, void* v, void* output,
                    void* stream) {
   if (plan == nullptr) throw std::runtime_error("feattn: null plan");
   check(fe_attn_run(plan->plan, q, k, v, output, lse, causal ? 1 : 0, stream));
+}
+
+void norm(const void* x, const void* residual, const void* weight, void* output, void* new_residual, int rows,
+          int width, float eps, bool bf16, void* stream) {
+  check(fe_norm(x, residual, weight, output, new_residual, rows, width, eps, bf16 ? 1 : 0, stream));
+}
+
+void silu_mul(const void* gu, void* output, int rows, int width, bool bf16, void* stream) {
+  check(fe_silu_mul(gu, output, rows, width, bf16 ? 1 : 0, stream));
+}
+
+void accept(const int64_t* draft, const int64_t* verify, int64_t* committed, int batch, int k, void* stream) {
+  check(fe_accept(draft, verify, committed, batch, k, stream));
+}
+
+void norm_rope_store(const void* qkv, int64_t row_stride, const void* q_weight, const void* k_weight, float eps,
+                     void* q_out, void* kc, void* vc, const int64_t* pos, const int64_t* slots, const float* cache,
+                     int rows, int hq, int hkv, int dim, bool bf16, void* stream, int max_positions,
+                     int cache_slots) {
+  check(fe_norm_rope_append(qkv, row_stride, q_weight, k_weight, eps, q_out, kc, vc, pos, slots, cache, rows, hq, hkv,
+                            dim, bf16 ? 1 : 0, max_positions, cache_slots, stream));
 }
 
 void rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim, bool bf16,

@@ -54,6 +54,14 @@ DRIVER_SYMBOLS = (
     "fe_rope_table",
 )
 
+# Every extern "C" symbol of include/fe_ops.h.
+OPS_SYMBOLS = (
+    "fe_norm",
+    "fe_silu_mul",
+    "fe_accept",
+    "fe_norm_rope_append",
+)
+
 _LIB: Optional[ctypes.CDLL] = None
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -106,6 +114,13 @@ def lib() -> ctypes.CDLL:
     L.fe_rope_table.argtypes = [_vp, _int, _int, ctypes.c_double, _vp]
     for name in DRIVER_SYMBOLS:
         getattr(L, name).restype = _i64 if name == "fe_blocks_used" else _int
+    _f = ctypes.c_float
+    L.fe_norm.argtypes = [_vp] * 5 + [_int, _int, _f, _int, _vp]
+    L.fe_silu_mul.argtypes = [_vp, _vp, _int, _int, _int, _vp]
+    L.fe_accept.argtypes = [_vp, _vp, _vp, _int, _int, _vp]
+    L.fe_norm_rope_append.argtypes = ([_vp, _i64, _vp, _vp, _f] + [_vp] * 6 + [_int] * 4 + [_int, _int, _int, _vp])
+    for name in OPS_SYMBOLS:
+        getattr(L, name).restype = _int
     _LIB = L
     return L
 
@@ -312,3 +327,35 @@ def rope_table(table, max_len: int, dim: int, theta: float, stream=None) -> None
     """Fills a device fp32 tensor [max_len, dim] with the cos | sin table
     (src/cuda_model.cpp:44-47)."""
     _check(lib().fe_rope_table(_ptr(table), max_len, dim, float(theta), _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# Per-token operators (include/fe_ops.h)
+# ---------------------------------------------------------------------------
+
+def norm(x, weight, output, rows: int, width: int, eps: float, bf16: bool, residual=None, new_residual=None,
+         stream=None) -> None:
+    """fe::cuda::norm (native_cuda.hpp:11): RMSNorm of [rows][width]."""
+    _check(lib().fe_norm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(output), _ptr(new_residual), rows, width,
+                         float(eps), int(bool(bf16)), _stream(stream)))
+
+
+def silu_mul(gate_up, output, rows: int, width: int, bf16: bool, stream=None) -> None:
+    """fe::cuda::silu_mul (native_cuda.hpp:12)."""
+    _check(lib().fe_silu_mul(_ptr(gate_up), _ptr(output), rows, width, int(bool(bf16)), _stream(stream)))
+
+
+def accept(draft, verify, out, batch: int, k: int, stream=None) -> None:
+    """fe::cuda::accept (native_cuda.hpp:15): int64 draft [batch][k], verify
+    [batch][k+1] -> out [batch][k+2]."""
+    _check(lib().fe_accept(_ptr(draft), _ptr(verify), _ptr(out), batch, k, _stream(stream)))
+
+
+def norm_rope_append(qkv, row_stride: int, q_weight, k_weight, eps: float, q_out, k_cache, v_cache, pos, slots,
+                     cache, rows: int, hq: int, hkv: int, bf16: bool, max_positions: int, cache_slots: int,
+                     dim: int = 128, stream=None) -> None:
+    """q/k RMSNorm + RoPE + paged append in one pass (src/cuda_model.cpp:91-95)."""
+    _check(lib().fe_norm_rope_append(_ptr(qkv), row_stride, _ptr(q_weight), _ptr(k_weight), float(eps),
+                                     _ptr(q_out), _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(slots), _ptr(cache),
+                                     rows, hq, hkv, dim, int(bool(bf16)), max_positions, cache_slots,
+                                     _stream(stream)))

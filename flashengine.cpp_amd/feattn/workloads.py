@@ -241,6 +241,15 @@ def decode_bytes(b: Batch, elem: int = 2) -> int:
     return ctx * kvb + q_o + page_ids
 
 
+def norm_rope_append_bytes(b: Batch, elem: int = 2) -> int:
+    """Fused q/k norm + RoPE + append per new token: the q|k|v projection
+    row read, q written, k and v cache writes, pos and slot reads, the cos|sin
+    row read (the two 128-element weights stay in cache)."""
+    per_row = ((b.hq + 2 * b.hkv) * HEAD_DIM * elem + b.hq * HEAD_DIM * elem + 2 * b.hkv * HEAD_DIM * elem
+               + 16 + HEAD_DIM * 4)
+    return b.rows * per_row
+
+
 def rope_append_bytes(b: Batch, elem: int = 2) -> int:
     """q read+write, k and v read, k and v cache writes, pos and slot reads,
     the cos|sin row read: per new token."""

@@ -12,9 +12,12 @@ Modules:
                   (src/cuda_kernels.cu:19-24, src/portable_gpu_ops.cpp:50-54).
   brute           float64 scalar-loop attention for tiny shapes; pins the
                   restatement independently of torch's kernels.
-  step_metadata   restatement of CudaModel::prepare's metadata and of
-                  graph_buckets (src/cuda_model.cpp:131-142,
-                  src/common.cpp:45-51).
+  step_metadata   restatement of CudaModel::prepare's metadata, graph_buckets
+                  and the FIFO page allocator (src/cuda_model.cpp:131-142,
+                  src/common.cpp:45-51, src/scheduler.cpp:5,31,35).
+  norm_ops        numpy restatement of RMSNorm, the SiLU-gated product,
+                  greedy acceptance and the fused q/k norm + rope + append
+                  (src/cuda_kernels.cu:11-18,25, src/cuda_model.cpp:91-95).
 
 Pinning (what each function is checked against) is listed in each module's
 docstring and exercised by tests/test_oracle_*.py.

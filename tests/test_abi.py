@@ -17,7 +17,7 @@ def header_functions(path):
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fe_\w+)\s*\(", text, flags=re.M)))
 
 
-HEADERS = {"fe_attn.h": feattn.C_SYMBOLS, "fe_driver.h": feattn.DRIVER_SYMBOLS}
+HEADERS = {"fe_attn.h": feattn.C_SYMBOLS, "fe_driver.h": feattn.DRIVER_SYMBOLS, "fe_ops.h": feattn.OPS_SYMBOLS}
 
 
 def test_header_matches_binding_list():
@@ -37,8 +37,9 @@ def test_library_exports_every_c_symbol():
 
 
 def test_library_exports_reference_namespace():
-    """fe::cuda:: symbols with the reference's exact parameter lists
-    (include/fe/native_cuda.hpp:7-14), so cuda_model.cpp can link unchanged."""
+    """fe::cuda:: symbols with the reference's exact parameter lists -- every
+    function of include/fe/native_cuda.hpp:7-15 -- so cuda_model.cpp can link
+    unchanged."""
     out = subprocess.run(["nm", "-DC", feattn.LIB_PATH], capture_output=True, text=True,
                          check=True).stdout
     want = [
@@ -49,6 +50,9 @@ def test_library_exports_reference_namespace():
         "fe::cuda::attention(fe::cuda::AttentionPlan*, void*, void*, void*, void*, bool, void*)",
         "fe::cuda::rope(void*, void*, long const*, float const*, int, int, int, int, bool, void*, int)",
         "fe::cuda::store(void const*, void const*, void*, void*, long const*, int, int, bool, void*, int)",
+        "fe::cuda::norm(void const*, void const*, void const*, void*, void*, int, int, float, bool, void*)",
+        "fe::cuda::silu_mul(void const*, void*, int, int, bool, void*)",
+        "fe::cuda::accept(long const*, long const*, long*, int, int, void*)",
     ]
     for w in want:
         assert w in out, w

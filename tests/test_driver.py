@@ -1,8 +1,8 @@
-"""Host driver (include/fe_driver.h) on the CPU: graph buckets and the KV page
-allocator against the reference's own host assertions
-(tests/host_tests.cpp:13,33), and the per-step metadata builder against the
-workload builder the attention tests use (src/cuda_model.cpp:131-142), bit
-for bit, graph padding and error cases included."""
+"""Host driver (include/fe_driver.h) on the CPU against oracle/step_metadata.py:
+graph buckets and the KV page allocator (both also checked against the
+reference's own host assertions, tests/host_tests.cpp:13,33), and the
+per-step metadata builder (src/cuda_model.cpp:131-142) bit for bit, graph
+padding and error cases included."""
 
 import ctypes
 
@@ -11,11 +11,18 @@ import pytest
 
 import feattn
 from feattn import workloads as W
+from oracle import step_metadata as S
 
 
 def test_graph_buckets_reference_assertion():
     # tests/host_tests.cpp:13
     assert feattn.graph_buckets(7) == [1, 2, 4, 7]
+    assert S.graph_buckets(7) == [1, 2, 4, 7]
+
+
+def test_graph_buckets_match_oracle():
+    for maximum in range(1, 600):
+        assert feattn.graph_buckets(maximum) == S.graph_buckets(maximum), maximum
 
 
 @pytest.mark.parametrize("maximum", [1, 2, 3, 8, 9, 15, 16, 17, 64, 100, 256, 1000])
@@ -41,20 +48,37 @@ def test_graph_buckets_rejects_nonpositive():
             feattn.graph_buckets(bad)
 
 
-def test_blocks_reference_assertions():
+@pytest.mark.parametrize("impl", ["native", "oracle"])
+def test_blocks_reference_assertions(impl):
     # tests/host_tests.cpp:33: BlockManager(2,16); a needs 2 pages for 17
     # tokens, b cannot get one, nothing is taken on failure; release frees all
-    blocks = feattn.Blocks(2, 16)
+    blocks = feattn.Blocks(2, 16) if impl == "native" else S.Blocks(2, 16)
+    table = blocks.table if impl == "native" else (lambda s: blocks.tables.get(s, []))
     a, b = 1, 2
     assert blocks.ensure(a, 17)
     assert not blocks.ensure(b, 1)
-    assert blocks.table(b) == []
+    assert table(b) == []
     blocks.release(a)
     assert blocks.used() == 0
     assert blocks.ensure(b, 1)
     blocks.release(b)
     assert blocks.used() == 0
-    blocks.close()
+
+
+def test_blocks_random_ops_match_oracle():
+    rng = np.random.default_rng(5)
+    native, ref = feattn.Blocks(97, 16), S.Blocks(97, 16)
+    for _ in range(3000):
+        seq = int(rng.integers(0, 12))
+        if rng.random() < 0.25:
+            native.release(seq)
+            ref.release(seq)
+        else:
+            target = int(rng.integers(0, 400))
+            assert native.ensure(seq, target) == ref.ensure(seq, target)
+        assert native.table(seq) == ref.tables.get(seq, [])
+        assert native.used() == ref.used()
+    native.close()
 
 
 def test_blocks_fifo_order_and_growth():
@@ -94,14 +118,26 @@ WORKLOADS = [W.qwen3_06b_decode, W.qwen3_8b_decode, W.qwen3_8b_prefill, W.qwen3_
              W.dflash_block]
 
 
+def _same(m, want):
+    for key in ("positions", "slots", "qo", "kv", "pages", "last"):
+        assert m[key].tolist() == want[key], key
+
+
 @pytest.mark.parametrize("make", WORKLOADS, ids=lambda f: f.__name__)
-def test_prepare_metadata_matches_builder(make):
+def test_prepare_metadata_matches_oracle(make):
     b = make()
+    _same(_via_driver(b), S.prepare(b.starts, b.qlens, b.tables, b.page, 1 << 20))
+    # the workload builder the attention tests use agrees too
     m = _via_driver(b)
-    assert np.array_equal(m["positions"], b.positions)
-    assert np.array_equal(m["slots"], b.slots)
-    assert m["qo"].tolist() == b.qo and m["kv"].tolist() == b.kv
-    assert m["pages"].tolist() == b.pages and m["last"].tolist() == b.last
+    assert np.array_equal(m["slots"], b.slots) and m["pages"].tolist() == b.pages
+
+
+@pytest.mark.parametrize("count,entry_rows", [(8, 1), (16, 4), (5, 16)])
+def test_prepare_metadata_padding_matches_oracle(count, entry_rows):
+    b = W.make_batch(32, 8, starts=[100, 7, 2000, 0, 33], qlens=[1, 4, 4, 16, 1], seed=11)
+    m = _via_driver(b, count=count, entry_rows=entry_rows, dummy_page=b.blocks)
+    _same(m, S.prepare(b.starts, b.qlens, b.tables, b.page, 1 << 20, count=count, entry_rows=entry_rows,
+                       dummy_page=b.blocks))
 
 
 def test_prepare_metadata_slots_closed_form():
