@@ -1,0 +1,121 @@
+"""GPU edge cases of fe_attn_run against the oracle: page sizes other than
+16, page-boundary lengths (len 1, len = page, len = page + 1, a chunk with no
+prefix), an empty batch, stale or poisoned cache slots outside every visible
+range (they must not leak into results: the reference kernel reads only
+visible tokens), and plan capacity limits.  Tolerance as in
+test_gpu_attention.py: |a-b| <= 1e-2 + 1e-2*|b|, LSE within 1e-3."""
+
+import math
+
+import pytest
+import torch
+
+import feattn
+from feattn import workloads as W
+from oracle import aten_attention as A
+
+pytestmark = pytest.mark.gpu
+
+
+def run(b, q, kc, vc, causal, dev, max_pages=None):
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, max(1, b.batch), max_pages or b.max_pages(),
+                       q.dtype == torch.bfloat16, b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    out = torch.zeros_like(qd)
+    lse = torch.full((b.rows, b.hq), float("nan"), device=dev)
+    plan.run(qd, kd, vd, out, causal=causal, lse=lse)
+    torch.cuda.synchronize()
+    plan.close()
+    return out.cpu(), lse.cpu()
+
+
+def check(out, lse, want_out, want_lse):
+    torch.testing.assert_close(out.float(), want_out.float(), atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(lse, want_lse, atol=1e-3, rtol=0)
+
+
+@pytest.mark.parametrize("page", [32, 64, 256])
+@pytest.mark.parametrize("causal", [True, False])
+def test_page_sizes(dev, page, causal):
+    b = W.make_batch(32, 8, starts=[page - 1, page, 3 * page + 5, 0, 2 * page - 3],
+                     qlens=[1, 1, 40, page + 3, 4], seed=page, extra_pages=2)
+    q, kc, vc = W.make_tensors(b, seed=page)
+    out, lse = run(b, q, kc, vc, causal, dev)
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    check(out, lse, want_out, want_lse)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_page_boundary_lengths(dev, dtype):
+    """len 1, len = page, len = page + 1, a 16-row chunk with no prefix, a
+    chunk ending exactly on a page boundary, one 64-token tile exactly."""
+    b = W.make_batch(32, 8, starts=[0, 15, 16, 0, 16, 63, 0], qlens=[1, 1, 1, 16, 16, 1, 64], seed=5)
+    q, kc, vc = W.make_tensors(b, seed=5, dtype=dtype)
+    for causal in (True, False):
+        out, lse = run(b, q, kc, vc, causal, dev)
+        want_out, want_lse = A.run(b, q, kc, vc, causal)
+        check(out, lse, want_out, want_lse)
+    # a single visible token: softmax weight 1, out = v, lse = scaled score
+    r = b.qo[0]
+    v0 = vc[b.tables[0][0], 0].float().repeat_interleave(4, 0)
+    out, lse = run(b, q, kc, vc, True, dev)
+    torch.testing.assert_close(out[r].float(), v0, atol=1e-2, rtol=1e-2)
+    k0 = kc[b.tables[0][0], 0].float().repeat_interleave(4, 0)
+    want_lse0 = (q[r].float() * k0).sum(-1) / math.sqrt(128)
+    torch.testing.assert_close(lse[r], want_lse0, atol=1e-3, rtol=0)
+
+
+def test_empty_batch_is_a_no_op(dev):
+    plan = feattn.Plan(32, 8, 128, 16, 4, 8, True, 16)
+    plan.prepare([0], [0], [], [], 0, 0)
+    q = torch.zeros(1, 32, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(17, 16, 8, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.full_like(q, 7.0)
+    plan.run(q, kc, kc, out, causal=True)
+    torch.cuda.synchronize()
+    assert (out == 7.0).all()
+    plan.close()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_stale_slots_do_not_leak(dev, causal):
+    """Every cache slot outside the visible ranges (the rest of each last
+    page, unused pool pages, the dummy page) holds NaN; the results must be
+    those of a cache holding zeros there."""
+    b = W.make_batch(32, 8, starts=[700, 5, 33, 0, 2000], qlens=[1, 3, 50, 20, 16], seed=9, extra_pages=6)
+    q, kc, vc = W.make_tensors(b, seed=9)
+    live = torch.zeros(b.blocks + 1, b.page, dtype=torch.bool)
+    for s in range(b.batch):
+        for t in range(b.lens[s]):
+            live[b.tables[s][t // b.page], t % b.page] = True
+    kz, vz = kc.clone(), vc.clone()
+    kz[~live] = 0
+    vz[~live] = 0
+    kn, vn = kc.clone(), vc.clone()
+    kn[~live] = float("nan")
+    vn[~live] = float("nan")
+    out, lse = run(b, q, kn, vn, causal, dev)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    want_out, want_lse = A.run(b, q, kz, vz, causal)
+    check(out, lse, want_out, want_lse)
+
+
+def test_capacity_limits(dev):
+    """max_batch sequences at the longest context the plan admits
+    ((max_pages - 1) * page tokens) run; one token more is refused."""
+    max_pages = 9
+    ctx = (max_pages - 1) * 16
+    b = W.make_batch(32, 8, starts=[ctx - 1] * 3, qlens=[1] * 3, seed=2)
+    q, kc, vc = W.make_tensors(b, seed=2)
+    out, lse = run(b, q, kc, vc, True, dev, max_pages=max_pages)
+    want_out, want_lse = A.run(b, q, kc, vc, True, max_pages=max_pages)
+    check(out, lse, want_out, want_lse)
+    plan = feattn.Plan(32, 8, 128, 16, 3, max_pages, True, b.blocks)
+    too_long = W.make_batch(32, 8, starts=[ctx] * 3, qlens=[1] * 3, seed=2)
+    with pytest.raises(RuntimeError):
+        plan.prepare(too_long.qo, too_long.kv, too_long.pages, too_long.last, 3, 3)
+    four = W.make_batch(32, 8, starts=[10] * 4, qlens=[1] * 4, seed=2)
+    with pytest.raises(RuntimeError):
+        plan.prepare(four.qo, four.kv, four.pages, four.last, 4, 4)
+    plan.close()
