@@ -377,8 +377,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
         x[r] = tok + 4 * J + r <= lim ? sc[r] * a.scale_log2 : kNegInf;
         mx = fmaxf(mx, x[r]);
       }
-      mx = fmaxf(mx, xor16(mx));
-      mx = fmaxf(mx, xor32(mx));
+      mx = max_x32(max_x16(mx));
       // Lazy reference maximum: raised (with l and o rescaled) only when the
       // block maximum exceeds it by more than 8, so p <= 2^8.
       const bool up = mx > m + 8.f;
@@ -417,8 +416,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       r_slot = v_slot + 1 == U ? 0 : v_slot + 1;
     }
 
-    lsum += xor16(lsum);
-    lsum += xor32(lsum);
+    lsum = sum_x32(sum_x16(lsum));
     if (col_ok) {
       const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
       const float l2 = lsum > 0.f ? m + __log2f(lsum) : kNegInf;
@@ -579,8 +577,7 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
           }
           mx = fmaxf(mx, sc[tb][cb][r]);
         }
-      mx = fmaxf(mx, xor16(mx));
-      mx = fmaxf(mx, xor32(mx));
+      mx = max_x32(max_x16(mx));
       // Lazy reference maximum: raised (with l and o rescaled) only when the
       // tile maximum exceeds it by more than 8, so p <= 2^8.
       const float mt = mx * a.scale_log2;
@@ -654,8 +651,7 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
       float ln = lsum[cb];
-      ln += xor16(ln);
-      ln += xor32(ln);
+      ln = sum_x32(sum_x16(ln));
       const int n = wave * kWcols + 16 * cb + L;
       if (n < ncols) {
         const float inv = ln > 0.f ? 1.f / ln : 0.f;

@@ -108,6 +108,29 @@ __device__ __forceinline__ float xor32(float v) {
   return __shfl_xor(v, 32, 64);
 }
 
+// Reductions over lane pairs (i, i ^ 16) and (i, i ^ 32) on the VALU with
+// gfx950's v_permlane{16,32}_swap (no LDS round trip).  Swapping a value
+// with itself yields {rows 0,0,2,2} and {rows 1,1,3,3} (16-lane rows) for
+// permlane16, {lower, lower} and {upper, upper} (32-lane halves) for
+// permlane32, so combining the two results gives every lane the reduction
+// of its pair, with the same operand order in both lanes of the pair.
+__device__ __forceinline__ float max_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
