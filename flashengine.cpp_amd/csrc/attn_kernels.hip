@@ -708,17 +708,19 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
     }
   }
 
-  // Items it, it + gridDim.x, ...; each item's first tile is requested
-  // during the previous item's last tile.
-  int it = blockIdx.x;
-  if (it >= n_items) return;
+  // The workgroup's share of the item list (assigned by the planner,
+  // longest items first); each item's first tile is requested during the
+  // previous item's last tile.
+  int it = ldc(a.tile_off, blockIdx.x);
+  const int end = min(ldc(a.tile_off, blockIdx.x + 1), n_items);
+  if (it >= end) return;
   WorkItem w = ldc_item(a.items, it);
   SeqInfo s = ldc_seq(a.seqs, w.seq);
   tile_copy(a, w, s, tl, lbase, wave, w.t0, 0);
   int stage = 0;
   for (;;) {
-    const int nit = it + gridDim.x;
-    const bool has_next = nit < n_items;
+    const int nit = it + 1;
+    const bool has_next = nit < end;
     WorkItem wn = w;
     SeqInfo sn = s;
     if (has_next) {

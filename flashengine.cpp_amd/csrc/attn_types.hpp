@@ -92,6 +92,7 @@ struct AttnArgs {
   const int32_t* pages;
   const WorkItem* items;
   const int32_t* n_items;  // device-resident count (graph replays read the current one)
+  const int32_t* tile_off;   // tile only: items of workgroup b = [tile_off[b], tile_off[b+1])
   const DecodeItem* ditems;  // decode only: the pieces, share by share
   const ShareStart* shares;  // decode only: one record per share
   int n_share_cap;           // decode only: records in `shares`

@@ -67,7 +67,7 @@ int share_cap(const PlanShape& sh) { return std::max(1, sh.decode_waves / sh.hkv
 
 // Offsets of the regions inside the metadata arena (same layout on host and device).
 struct Layout {
-  size_t seqs, pages, counts, dshare, decode, tile[2], merge[2], total;
+  size_t seqs, pages, counts, dshare, decode, tile[2], tshare[2], merge[2], total;
 };
 
 Layout make_layout(const PlanShape& sh) {
@@ -86,6 +86,8 @@ Layout make_layout(const PlanShape& sh) {
   for (int m = 0; m < 2; ++m) {
     l.tile[m] = off;
     off = align256(off + sizeof(WorkItem) * sh.item_cap);
+    l.tshare[m] = off;
+    off = align256(off + sizeof(int32_t) * ((size_t)sh.tile_slots + 1));
   }
   for (int m = 0; m < 2; ++m) {
     l.merge[m] = off;
@@ -124,6 +126,7 @@ struct fe_attn_plan {
   bool graph = false;
   int graph_nc = 0;
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
+  int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;  // wavefronts per decode workgroup
   int decode_nc = 4;
   int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
@@ -161,6 +164,7 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   sh.num_cus = cus > 0 ? cus : 256;
 
   sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
+  sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
   auto* p = new fe_attn_plan();
   p->sh = sh;
   p->bf16 = bf16 != 0;
@@ -168,7 +172,7 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   p->lay = make_layout(sh);
   p->decode_wg = decode_wg_waves(hkv);
   p->grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / p->decode_wg;  // persistent: every workgroup resident
-  p->grid_tile_cap = sh.num_cus * 2;    // 2 resident 256-thread tile workgroups per CU
+  p->grid_tile_cap = sh.tile_slots;
   p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head) pairs per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
     fe_attn_plan_destroy(p);
@@ -246,9 +250,17 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
   cnt[kCntMerge1] = (int32_t)bp.mode[1].merge.size();
   std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
+  const int tslots = p->sh.tile_slots;
   for (int m = 0; m < 2; ++m) {
     std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
     std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
+    // share offsets up to the launch capacity: shares past those in use are
+    // empty (a graph launch covers every slot)
+    const std::vector<int32_t>& off = bp.mode[m].tile_off;
+    const int used = off.empty() ? 0 : (int)off.size() - 1;
+    if (used > tslots) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: tile shares");
+    int32_t* dst = reinterpret_cast<int32_t*>(h + l.tshare[m]);
+    for (int k = 0; k <= tslots; ++k) dst[k] = k <= used && !off.empty() ? off[k] : (int32_t)bp.mode[m].tile.size();
   }
   auto copy = [&](size_t off, size_t bytes) -> hipError_t {
     if (bytes == 0) return hipSuccess;
@@ -262,6 +274,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e == hipSuccess) e = copy(l.decode, sizeof(DecodeItem) * bp.decode_items.size());
   for (int m = 0; m < 2 && e == hipSuccess; ++m) {
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
+    if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * ((size_t)tslots + 1));
     if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
   }
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
@@ -274,6 +287,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   p->n_decode = n_shares * p->sh.hkv;  // busy decode wavefronts
   for (int m = 0; m < 2; ++m) {
     p->n_tile[m] = (int)bp.mode[m].tile.size();
+    p->n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
     p->n_merge[m] = (int)bp.mode[m].merge.size();
   }
   return FE_OK;
@@ -321,7 +335,8 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     AttnArgs t = a;
     t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.tile[mode]);
     t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
-    const int grid = p->graph ? p->grid_tile_cap : std::min(p->grid_tile_cap, p->n_tile[mode]);
+    t.tile_off = reinterpret_cast<const int32_t*>(p->dev + p->lay.tshare[mode]);
+    const int grid = p->graph ? p->grid_tile_cap : p->n_tshare[mode];
     e = launch_tile(t, p->bf16, causal != 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "tile kernel launch");
   }

@@ -30,10 +30,36 @@ std::vector<int64_t> cut_uniform(int64_t stream, int64_t quota) {
   return cuts;
 }
 
-// Sorts by decreasing cost so the longest items start first (LPT order).
-void order_items(std::vector<WorkItem>& items) {
+// Assigns items to `slots` shares (one per tile workgroup) by the longest
+// processing time rule -- in decreasing cost order, each item goes to the
+// least-loaded share -- and regroups them share by share (longest first
+// inside a share).  off receives the CSR offsets of the shares in use.
+void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off) {
   std::stable_sort(items.begin(), items.end(),
                    [](const WorkItem& x, const WorkItem& y) { return x.cost > y.cost; });
+  const int n = std::max(1, std::min<int>(slots, (int)items.size()));
+  std::vector<int64_t> load(n, 0);
+  std::vector<int> share(items.size());
+  // (load, share) min-heap
+  std::vector<std::pair<int64_t, int>> heap;
+  heap.reserve(n);
+  for (int k = 0; k < n; ++k) heap.emplace_back(0, k);
+  auto cmp = [](const std::pair<int64_t, int>& x, const std::pair<int64_t, int>& y) { return x > y; };
+  std::make_heap(heap.begin(), heap.end(), cmp);
+  for (size_t i = 0; i < items.size(); ++i) {
+    std::pop_heap(heap.begin(), heap.end(), cmp);
+    auto& top = heap.back();
+    share[i] = top.second;
+    top.first += items[i].cost;
+    std::push_heap(heap.begin(), heap.end(), cmp);
+  }
+  off.assign(n + 1, 0);
+  for (size_t i = 0; i < items.size(); ++i) ++off[share[i] + 1];
+  for (int k = 0; k < n; ++k) off[k + 1] += off[k];
+  std::vector<WorkItem> grouped(items.size());
+  std::vector<int32_t> pos(off.begin(), off.end() - 1);
+  for (size_t i = 0; i < items.size(); ++i) grouped[pos[share[i]]++] = items[i];
+  items.swap(grouped);
 }
 
 }  // namespace
@@ -275,9 +301,9 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
           for (int sp = 0; sp < ns; ++sp) {
             const int t0 = sp * chunk;
             const int t1 = std::min(extent, t0 + chunk);
-            // Cost ~ MFMA work: visible tokens times columns (the causal
-            // diagonal tile counted in full).
-            const int cost = (t1 - t0) / 16 * nq * G / 16 + 1;
+            // Cost ~ tiles times the 16-column blocks each wavefront
+            // computes (1 for items of <= 64 columns, else 2).
+            const int cost = ceil_div(t1 - t0, kTileTokens) * (nq * G > kTileCols / 2 ? 2 : 1);
             for (int h = 0; h < sh.hkv; ++h)
               ml.tile.push_back(WorkItem{b, s.qo + i0, nq, h, t0, t1, base < 0 ? -1 : base + sp * nq, cost});
           }
@@ -290,7 +316,7 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
       }
       want = std::max(1, want / 2);
     }
-    order_items(ml.tile);
+    assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
   }
   for (int causal = 0; causal < 2; ++causal) {
     std::vector<MergeRow>& m = out.mode[causal].merge;

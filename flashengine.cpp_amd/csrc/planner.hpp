@@ -21,12 +21,14 @@ struct PlanShape {
   int blocks = 0;
   int num_cus = 256;        // compute units on the device (sizes split-KV)
   int decode_waves = 2048;  // wavefront slots of one decode launch
+  int tile_slots = 512;     // workgroups of one tile launch (two resident per CU)
   int item_cap = 1 << 16;   // work items per list
   int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
 };
 
 struct ModeLists {
-  std::vector<WorkItem> tile;
+  std::vector<WorkItem> tile;            // grouped by share: share k = [tile_off[k], tile_off[k+1])
+  std::vector<int32_t> tile_off;         // CSR over shares (one share per tile workgroup)
   std::vector<MergeRow> merge;
   int partial_rows = 0;  // decode partials followed by this mode's tile partials
 };
