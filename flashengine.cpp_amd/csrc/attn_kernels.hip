@@ -739,35 +739,43 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
 // ===========================================================================
 // Split-KV merge
 // ===========================================================================
-// One wavefront per (merged row, head); lane owns 2 of the 128 dims.  Splits
-// are folded in batches of 16 whose log-sum-exps and partial rows are all in
-// flight together.
+// One wavefront per (merged row, pair of heads): lanes 0-31 take head 2hp,
+// lanes 32-63 head 2hp + 1, each lane 4 of the 128 dims, so every partial-row
+// load is one 16-byte access per lane.  Splits are folded in batches of
+// kMergeBatch whose log-sum-exps and partial rows are all in flight
+// together; loads past a row's split count are not issued.
 template <bool BF16>
 __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
   const int lane = threadIdx.x & 63;
   const int hq = a.hq;
+  const int hpairs = (hq + 1) >> 1;
   const int stride = gridDim.x * 4;
   int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
   // The first row record is requested together with the row count (its
   // index is clamped into the buffer; it is used only below the count).
-  MergeRow mr = a.rows[min(pair / hq, a.rows_cap - 1)];
-  const int n_pairs = uniform(*a.n_rows) * hq;
+  MergeRow mr = a.rows[min(pair / hpairs, a.rows_cap - 1)];
+  const int n_pairs = uniform(*a.n_rows) * hpairs;
+  const int d = 4 * (lane & 31);
   for (; pair < n_pairs; pair += stride) {
-    if (pair >= stride) mr = a.rows[pair / hq];
-    const int h = pair % hq;
-    // Online merge over batches of kMergeBatch splits; each batch's
-    // log-sum-exps and partial rows are all requested before any is used.
-    constexpr int kMergeBatch = 16;
-    float m = kNegInf, wsum = 0.f, o0 = 0.f, o1 = 0.f;
+    if (pair >= stride) mr = a.rows[pair / hpairs];
+    const int h = 2 * (pair % hpairs) + (lane >> 5);
+    const bool on = h < hq;
+    const int hh = on ? h : hq - 1;
+    constexpr int kMergeBatch = 8;
+    float m = kNegInf, wsum = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = 0; sp0 < mr.nsplit; sp0 += kMergeBatch) {
       float l[kMergeBatch];
-      float2 v[kMergeBatch];
+      f32x4 v[kMergeBatch];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
-        const int sp = min(sp0 + u, mr.nsplit - 1);
-        const size_t slot = (size_t)(mr.part + sp * mr.stride);
-        l[u] = sp0 + u < mr.nsplit ? a.part_lse[slot * hq + h] : kNegInf;
-        v[u] = *reinterpret_cast<const float2*>(a.part_o + (slot * hq + h) * kHeadDim + 2 * lane);
+        l[u] = kNegInf;
+        v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (sp0 + u < mr.nsplit) {  // wave-uniform
+          const size_t slot = (size_t)(mr.part + (sp0 + u) * mr.stride);
+          l[u] = a.part_lse[slot * hq + hh];
+          v[u] = *reinterpret_cast<const f32x4*>(a.part_o + (slot * hq + hh) * kHeadDim + d);
+        }
       }
       float bm = m;
 #pragma unroll
@@ -775,21 +783,22 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
       const float mu = bm == kNegInf ? 0.f : bm;
       const float sc = fast_exp2(m - mu);
       wsum *= sc;
-      o0 *= sc;
-      o1 *= sc;
+      acc *= sc;
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         const float wt = fast_exp2(l[u] - mu);
         wsum += wt;
-        o0 += wt * v[u].x;
-        o1 += wt * v[u].y;
+        acc += wt * v[u];
       }
       m = bm;
     }
-    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-    const size_t oi = (size_t)mr.row * hq + h;
-    *reinterpret_cast<uint32_t*>(a.out + oi * kHeadDim + 2 * lane) = pack2<BF16>(o0 * inv, o1 * inv);
-    if (a.lse != nullptr && lane == 0) a.lse[oi] = wsum > 0.f ? (m + __log2f(wsum)) * kLn2 : kNegInf;
+    if (on) {
+      const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+      const size_t oi = (size_t)mr.row * hq + h;
+      const u32x2 o = {pack2<BF16>(acc[0] * inv, acc[1] * inv), pack2<BF16>(acc[2] * inv, acc[3] * inv)};
+      *reinterpret_cast<u32x2*>(a.out + oi * kHeadDim + d) = o;
+      if (a.lse != nullptr && (lane & 31) == 0) a.lse[oi] = wsum > 0.f ? (m + __log2f(wsum)) * kLn2 : kNegInf;
+    }
   }
 }
 

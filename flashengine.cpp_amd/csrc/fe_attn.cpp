@@ -173,7 +173,7 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   p->decode_wg = decode_wg_waves(hkv);
   p->grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / p->decode_wg;  // persistent: every workgroup resident
   p->grid_tile_cap = sh.tile_slots;
-  p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head) pairs per workgroup
+  p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head pair) units per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
     fe_attn_plan_destroy(p);
     return fail(code, msg);
@@ -350,7 +350,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     m.part_o = p->part_o;
     m.part_lse = p->part_lse;
     m.hq = p->sh.hq;
-    const int pairs4 = (int)(((int64_t)p->n_merge[mode] * p->sh.hq + 3) / 4);
+    const int pairs4 = (int)(((int64_t)p->n_merge[mode] * ((p->sh.hq + 1) / 2) + 3) / 4);
     const int grid = p->graph ? p->grid_merge_cap : std::min(p->grid_merge_cap, pairs4);
     e = launch_merge(m, p->bf16, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
