@@ -181,7 +181,10 @@ __device__ __forceinline__ ShareStart ldc_share(const ShareStart* shares, int i)
   return r;
 }
 
-template <bool BF16, int WAVES>
+// NCB: 16-column blocks per item (1 or 2: up to 32 (query row, head)
+// columns, e.g. 8 verify rows with 4 heads per kv head).  Four blocks would
+// need more than the 256 registers of two wavefronts per SIMD.
+template <bool BF16, int WAVES, int NCB>
 __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int causal) {
   constexpr int U = dec_units<WAVES>();
   static_assert(U >= 2, "the ring must hold one K/V pair");
@@ -251,6 +254,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
   DecodeItem nw = cw;
   if (c_it + 1 < it_end) nw = ldc_ditem(a.ditems, c_it + 1);
   int c_kind = 0;
+  int c_qb = 0;  // column block of the next Q unit
   int c_tok = cw.t0;
   int pg_next = rec.pg0;
   int pg_after = rec.pg1;  // page of the block after pg_next's, valid while first_k
@@ -266,13 +270,17 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       const int nc = cw.nq * G;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int n = 4 * r + J;
-        const int nn = n < nc ? n : 0;  // columns past the item repeat column 0
+        const int n = 4 * r + J;  // row of the unit = column within the block
+        const int col = 16 * c_qb + n;
+        const int nn = col < nc ? col : 0;  // columns past the item repeat column 0
         const int row = cw.q0 + nn / G;
         const int head = kvh * G + nn % G;
         lds_dma16(a.q + ((size_t)row * a.hq + head) * kHeadDim + 8 * (L ^ n), dst + 1024 * r);
       }
-      c_kind = 1;
+      if (++c_qb == NCB) {
+        c_qb = 0;
+        c_kind = 1;
+      }
     } else if (c_kind == 1) {
       pg_cur = pg_next;
       const char* kb = block_addr(a.kc, c_tok, pg_cur);
@@ -326,34 +334,43 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
     const int t0 = w.t0;
     const int t1 = w.t1;
     const int ncols = w.nq * G;
-    const bool col_ok = L < ncols;
-    const int crow = w.q0 + (col_ok ? L / G : 0);
-    const int chead = kvh * G + (col_ok ? L % G : 0);
-    int lim = -1;  // last visible token of column L
-    if (col_ok) {
-      lim = causal ? w.len - w.nq + (crow - w.q0) : w.len - 1;
-      lim = min(lim, t1 - 1);
+    bool col_ok[NCB];
+    int crow[NCB], chead[NCB], lim[NCB];  // lim: last visible token of the lane's column
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int n = 16 * cb + L;
+      col_ok[cb] = n < ncols;
+      crow[cb] = w.q0 + (col_ok[cb] ? n / G : 0);
+      chead[cb] = kvh * G + (col_ok[cb] ? n % G : 0);
+      lim[cb] = -1;
+      if (col_ok[cb]) lim[cb] = min(causal ? w.len - w.nq + (crow[cb] - w.q0) : w.len - 1, t1 - 1);
     }
 
-    // Q unit
-    wait_units<U>(issued - consumed - 1);
-    u32x4 qf[4];
-    {
+    // Q units, one per column block
+    u32x4 qf[NCB][4];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      if (cb > 0) refill();
+      wait_units<U>(issued - consumed - 1);
       const uint32_t qb = ring + (uint32_t)(r_slot * kDecUnit);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        qf[k] = lds_read16(qb + k_lds[k]);
-        if (!col_ok) qf[k] = u32x4{0u, 0u, 0u, 0u};
+        qf[cb][k] = lds_read16(qb + k_lds[k]);
+        if (!col_ok[cb]) qf[cb][k] = u32x4{0u, 0u, 0u, 0u};
       }
+      consumed += 1;
+      r_slot = r_slot + 1 == U ? 0 : r_slot + 1;
     }
-    consumed += 1;
-    r_slot = r_slot + 1 == U ? 0 : r_slot + 1;
 
-    float m = kNegInf;
-    float lsum = 0.f;
-    f32x4 o[8];
+    float m[NCB], lsum[NCB];
+    f32x4 o[8][NCB];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < NCB; ++cb) {
+      m[cb] = kNegInf;
+      lsum[cb] = 0.f;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) o[db][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (int tok = t0; tok < t1; tok += 16) {
       // The workgroup's wavefronts (consecutive kv heads of one share, the
@@ -366,32 +383,45 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       const int v_slot = r_slot + 1 == U ? 0 : r_slot + 1;
       const uint32_t vst = ring + (uint32_t)(v_slot * kDecUnit);
 
-      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+      f32x4 sc[NCB];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sc = mfma16<BF16>(lds_read16(kst + k_lds[k]), qf[k], sc);
+      for (int cb = 0; cb < NCB; ++cb) sc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const u32x4 kf = lds_read16(kst + k_lds[k]);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) sc[cb] = mfma16<BF16>(kf, qf[cb][k], sc[cb]);
+      }
 
-      float x[4];
-      float mx = kNegInf;
+      u32x2 pf[NCB];
+      float alpha[NCB];
+      bool any_up = false;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = tok + 4 * J + r <= lim ? sc[r] * a.scale_log2 : kNegInf;
-        mx = fmaxf(mx, x[r]);
-      }
-      mx = max_x32(max_x16(mx));
-      // Lazy reference maximum: raised (with l and o rescaled) only when the
-      // block maximum exceeds it by more than 8, so p <= 2^8.
-      const bool up = mx > m + 8.f;
-      const float alpha = up ? fast_exp2(m - mx) : 1.f;
-      if (up) m = mx;
-      const float m_use = m == kNegInf ? 0.f : m;
-      float ps = 0.f;
+      for (int cb = 0; cb < NCB; ++cb) {
+        float x[4];
+        float mx = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = fast_exp2(x[r] - m_use);
-        ps += x[r];
+        for (int r = 0; r < 4; ++r) {
+          x[r] = tok + 4 * J + r <= lim[cb] ? sc[cb][r] * a.scale_log2 : kNegInf;
+          mx = fmaxf(mx, x[r]);
+        }
+        mx = max_x32(max_x16(mx));
+        // Lazy reference maximum: raised (with l and o rescaled) only when the
+        // block maximum exceeds it by more than 8, so p <= 2^8.
+        const bool up = mx > m[cb] + 8.f;
+        alpha[cb] = up ? fast_exp2(m[cb] - mx) : 1.f;
+        if (up) m[cb] = mx;
+        any_up = any_up || up;
+        const float m_use = m[cb] == kNegInf ? 0.f : m[cb];
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[r] = fast_exp2(x[r] - m_use);
+          ps += x[r];
+        }
+        lsum[cb] = lsum[cb] * alpha[cb] + ps;
+        pf[cb] = u32x2{pack2<BF16>(x[0], x[1]), pack2<BF16>(x[2], x[3])};
       }
-      lsum = lsum * alpha + ps;
-      const u32x2 pf = {pack2<BF16>(x[0], x[1]), pack2<BF16>(x[2], x[3])};
 
       if (t1 - tok < 16) {
         // Rows past the item end hold stale cache contents: zero them so that
@@ -403,37 +433,45 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
           if ((q >> 4) >= t1 - tok) lds_zero16(vst + 16 * q);
         }
       }
-      if (__builtin_amdgcn_ballot_w64(up) != 0) {
+      if (__builtin_amdgcn_ballot_w64(any_up) != 0) {
 #pragma unroll
-        for (int db = 0; db < 8; ++db) o[db] *= alpha;
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+          for (int db = 0; db < 8; ++db) o[db][cb] *= alpha[cb];
       }
       u32x2 vf[8];
 #pragma unroll
       for (int db = 0; db < 8; ++db) vf[db] = lds_read_tr16(vst + v_lds[db]);
 #pragma unroll
-      for (int db = 0; db < 8; ++db) o[db] = mfma16k16<BF16>(vf[db], pf, o[db]);
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) o[db][cb] = mfma16k16<BF16>(vf[db], pf[cb], o[db][cb]);
       consumed += 2;
       r_slot = v_slot + 1 == U ? 0 : v_slot + 1;
     }
 
-    lsum = sum_x32(sum_x16(lsum));
-    if (col_ok) {
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      const float l2 = lsum > 0.f ? m + __log2f(lsum) : kNegInf;
-      if (w.part < 0) {
-        uint16_t* op = a.out + ((size_t)crow * a.hq + chead) * kHeadDim + 4 * J;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          const u32x2 v = {pack2<BF16>(o[db][0] * inv, o[db][1] * inv), pack2<BF16>(o[db][2] * inv, o[db][3] * inv)};
-          *reinterpret_cast<u32x2*>(op + 16 * db) = v;
+    for (int cb = 0; cb < NCB; ++cb) {
+      const float ls = sum_x32(sum_x16(lsum[cb]));
+      if (col_ok[cb]) {
+        const float inv = ls > 0.f ? 1.f / ls : 0.f;
+        const float l2 = ls > 0.f ? m[cb] + __log2f(ls) : kNegInf;
+        if (w.part < 0) {
+          uint16_t* op = a.out + ((size_t)crow[cb] * a.hq + chead[cb]) * kHeadDim + 4 * J;
+#pragma unroll
+          for (int db = 0; db < 8; ++db) {
+            const u32x2 v = {pack2<BF16>(o[db][cb][0] * inv, o[db][cb][1] * inv),
+                             pack2<BF16>(o[db][cb][2] * inv, o[db][cb][3] * inv)};
+            *reinterpret_cast<u32x2*>(op + 16 * db) = v;
+          }
+          if (a.lse != nullptr && J == 0) a.lse[(size_t)crow[cb] * a.hq + chead[cb]] = l2 * kLn2;
+        } else {
+          const size_t pslot = (size_t)(w.part + (16 * cb + L) / G);
+          float* po = a.part_o + (pslot * a.hq + chead[cb]) * kHeadDim + 4 * J;
+#pragma unroll
+          for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db][cb] * inv;
+          if (J == 0) a.part_lse[pslot * a.hq + chead[cb]] = l2;
         }
-        if (a.lse != nullptr && J == 0) a.lse[(size_t)crow * a.hq + chead] = l2 * kLn2;
-      } else {
-        const size_t pslot = (size_t)(w.part + L / G);
-        float* po = a.part_o + (pslot * a.hq + chead) * kHeadDim + 4 * J;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db] * inv;
-        if (J == 0) a.part_lse[pslot * a.hq + chead] = l2;
       }
     }
   }
@@ -813,28 +851,43 @@ int decode_wg_waves(int hkv) {
   return 1;
 }
 
-template <bool BF16, int WAVES>
+template <bool BF16, int WAVES, int NCB>
 static hipError_t decode_launch(const AttnArgs& a, int causal, int grid, hipStream_t st) {
   const size_t lds = (size_t)WAVES * dec_units<WAVES>() * kDecUnit + 16;
   static bool lds_ok = false;  // the ring may exceed the 64 KB default
   if (!lds_ok) {
-    const hipError_t e = hipFuncSetAttribute((const void*)attn_decode_kernel<BF16, WAVES>,
+    const hipError_t e = hipFuncSetAttribute((const void*)attn_decode_kernel<BF16, WAVES, NCB>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     lds_ok = true;
   }
-  hipLaunchKernelGGL((attn_decode_kernel<BF16, WAVES>), dim3(grid), dim3(64 * WAVES), lds, st, a, causal);
+  hipLaunchKernelGGL((attn_decode_kernel<BF16, WAVES, NCB>), dim3(grid), dim3(64 * WAVES), lds, st, a, causal);
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int causal, int grid, hipStream_t st) {
-  switch (waves) {
-    case 8: return bf16 ? decode_launch<true, 8>(a, causal, grid, st) : decode_launch<false, 8>(a, causal, grid, st);
-    case 4: return bf16 ? decode_launch<true, 4>(a, causal, grid, st) : decode_launch<false, 4>(a, causal, grid, st);
-    case 2: return bf16 ? decode_launch<true, 2>(a, causal, grid, st) : decode_launch<false, 2>(a, causal, grid, st);
-    case 1: return bf16 ? decode_launch<true, 1>(a, causal, grid, st) : decode_launch<false, 1>(a, causal, grid, st);
+template <bool BF16, int WAVES>
+static hipError_t decode_launch_ncb(const AttnArgs& a, int ncb, int causal, int grid, hipStream_t st) {
+  switch (ncb) {
+    case 1: return decode_launch<BF16, WAVES, 1>(a, causal, grid, st);
+    case 2: return decode_launch<BF16, WAVES, 2>(a, causal, grid, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <bool BF16>
+static hipError_t decode_launch_waves(const AttnArgs& a, int waves, int ncb, int causal, int grid, hipStream_t st) {
+  switch (waves) {
+    case 8: return decode_launch_ncb<BF16, 8>(a, ncb, causal, grid, st);
+    case 4: return decode_launch_ncb<BF16, 4>(a, ncb, causal, grid, st);
+    case 2: return decode_launch_ncb<BF16, 2>(a, ncb, causal, grid, st);
+    case 1: return decode_launch_ncb<BF16, 1>(a, ncb, causal, grid, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st) {
+  return bf16 ? decode_launch_waves<true>(a, waves, ncb, causal, grid, st)
+              : decode_launch_waves<false>(a, waves, ncb, causal, grid, st);
 }
 
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st) {

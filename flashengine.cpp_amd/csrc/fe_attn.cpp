@@ -22,7 +22,7 @@
 #include "planner.hpp"
 
 namespace feattn {
-hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int causal, int grid, hipStream_t st);
+hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st);
 int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
@@ -128,7 +128,7 @@ struct fe_attn_plan {
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;  // wavefronts per decode workgroup
-  int decode_nc = 4;
+  int decode_nc = 16;
   int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
 };
 
@@ -328,7 +328,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     d.n_items = counts + kCntDecode;
     const int wv = p->decode_wg;
     const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + wv - 1) / wv);
-    e = launch_decode(d, p->bf16, p->decode_wg, causal ? 1 : 0, std::max(grid, 1), st);
+    e = launch_decode(d, p->bf16, p->decode_wg, p->decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
   if (p->graph || p->n_tile[mode] > 0) {

@@ -173,7 +173,8 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
       max_cols = std::max(max_cols, s.qlen * G);
     }
   }
-  out.decode_nc = max_cols <= 4 ? 4 : max_cols <= 8 ? 8 : 16;
+  // columns per decode item, in 16-column MFMA blocks: 1 or 2 blocks
+  out.decode_nc = max_cols <= 16 ? 16 : 32;
   const int n_static = std::max(1, sh.decode_waves / sh.hkv);
   if (stream > 0) {
     // Partial slots and pieces that a cut needs (a sequence overlapping

@@ -41,7 +41,7 @@ struct BuiltPlan {
   std::vector<ShareStart> decode_starts;  // one per share in use
   int decode_partials = 0;
   std::vector<MergeRow> decode_merge;
-  int decode_nc = 4;             // 4, 8 or 16 columns per decode item
+  int decode_nc = 16;            // 16 or 32 columns per decode item (MFMA column blocks x 16)
   ModeLists mode[2];             // [0] full (non-causal), [1] causal
 };
 

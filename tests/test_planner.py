@@ -30,7 +30,7 @@ def coverage(b, causal):
             assert t0 % 64 == 0
             assert nq * b.group <= 128
         else:
-            assert nq * b.group <= 16
+            assert nq * b.group <= 32  # at most two 16-column MFMA blocks
         for r in range(q0, q0 + nq):
             assert seq_of_row[r] == seq
             i = r - b.qo[seq]
