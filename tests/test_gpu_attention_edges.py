@@ -119,3 +119,77 @@ def test_capacity_limits(dev):
     with pytest.raises(RuntimeError):
         plan.prepare(four.qo, four.kv, four.pages, four.last, 4, 4)
     plan.close()
+
+
+
+@pytest.mark.parametrize("hq,hkv,starts,qlens", [
+    # 4 query heads per kv head: 16-row blocks (64 columns) beside narrow rows
+    (32, 8, [3000, 40, 700, 5000, 16], [16, 1, 9, 12, 3]),
+    # 8 per kv head, 3 kv heads: 64-, 40-, 8- and 56-column items
+    (24, 3, [2000, 100, 900, 17], [8, 5, 1, 7]),
+    # one kv head with 64 query heads: a single row is 64 columns
+    (64, 1, [4000, 33, 1500], [1, 1, 1]),
+])
+@pytest.mark.parametrize("causal", [True, False])
+def test_many_columns_per_kv_head(dev, hq, hkv, starts, qlens, causal):
+    """(row, head) column counts per kv head around the decode kernel's
+    limit of 32: 33..64-column items run as tile items beside decode items,
+    with an odd kv head count and with a single kv head."""
+    b = W.make_batch(hq, hkv, starts=starts, qlens=qlens, seed=hq + hkv, extra_pages=1)
+    q, kc, vc = W.make_tensors(b, seed=hq)
+    out, lse = run(b, q, kc, vc, causal, dev)
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    check(out, lse, want_out, want_lse)
+
+
+def test_graph_keeps_captured_decode_variant(dev):
+    """A graph captured on 8-row verify items (32 columns per kv head: the
+    two-block decode variant) replays single rows and 16-row blocks (tile
+    items) correctly; a graph captured on single rows refuses 8-row items
+    afterwards (reference refusal of layout changes:
+    src/flashinfer_attention.cu:32)."""
+    hq, hkv, blocks = 32, 8, 700
+    kc = torch.zeros(blocks + 1, 16, hkv, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = torch.zeros(64, hq, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros_like(q)
+    lse = torch.zeros(64, hq, device=dev)
+    plan = feattn.Plan(hq, hkv, 128, 16, 4, 200, True, blocks)
+
+    def load(bb, seed):
+        qq, kk, vv = W.make_tensors(bb, seed=seed)
+        kc.copy_(kk.to(dev))
+        vc.copy_(vv.to(dev))
+        q.zero_()
+        q[:bb.rows].copy_(qq.to(dev))
+        plan.prepare(bb.qo, bb.kv, bb.pages, bb.last, bb.batch, bb.rows, graph=True)
+        return qq, kk, vv
+
+    verify = W.make_batch(hq, hkv, starts=[900, 2000, 40, 1200], qlens=[8] * 4, seed=1, pool=blocks)
+    load(verify, 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.run(q, kc, vc, out, causal=True, lse=lse)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(q, kc, vc, out, causal=True, lse=lse)
+    steps = [W.make_batch(hq, hkv, starts=[3000, 5, 700, 1800], qlens=[1] * 4, seed=2, pool=blocks),
+             W.make_batch(hq, hkv, starts=[300, 1500, 60, 2500], qlens=[16] * 4, seed=3, pool=blocks),
+             verify]
+    for seed, bb in enumerate(steps, start=2):
+        qq, kk, vv = load(bb, seed)
+        graph.replay()
+        torch.cuda.synchronize()
+        want_out, want_lse = A.run(bb, qq, kk, vv, True)
+        check(out[:bb.rows].cpu(), lse[:bb.rows].cpu(), want_out, want_lse)
+    plan.close()
+
+    narrow = feattn.Plan(hq, hkv, 128, 16, 4, 200, True, blocks)
+    one = W.make_batch(hq, hkv, starts=[30, 60], qlens=[1, 1], seed=4, pool=blocks)
+    narrow.prepare(one.qo, one.kv, one.pages, one.last, one.batch, one.rows, graph=True)
+    with pytest.raises(RuntimeError):
+        narrow.prepare(verify.qo, verify.kv, verify.pages, verify.last, verify.batch, verify.rows, graph=True)
+    narrow.close()
