@@ -592,13 +592,16 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) sc[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 4; ++k) {
+      // one base per k-step; the block offsets fold into the instruction
+      const uint32_t kb = st + tl.k_lds[k];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
-        const u32x4 kf = lds_read16(st + tb * kTileBlock + tl.k_lds[k]);
+        const u32x4 kf = lds_read16(kb + tb * kTileBlock);
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) sc[tb][cb] = mfma16<BF16>(kf, qf[cb][k], sc[tb][cb]);
       }
+    }
 
     u32x4 pf[2][NCB];
 #pragma unroll
@@ -646,17 +649,19 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
       }
     }
 
-    const uint32_t vst = st + 4 * kTileBlock;
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+    for (int db = 0; db < 8; ++db) {
+      // one base per dim block; the block offsets fold into the instruction
+      const uint32_t vb = st + tl.v_lds[db];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const u32x2 lo = lds_read_tr16(vst + (2 * ks) * kTileBlock + tl.v_lds[db]);
-        const u32x2 hi = lds_read_tr16(vst + (2 * ks + 1) * kTileBlock + tl.v_lds[db]);
+        const u32x2 lo = lds_read_tr16(vb + (4 + 2 * ks) * kTileBlock);
+        const u32x2 hi = lds_read_tr16(vb + (5 + 2 * ks) * kTileBlock);
         const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) o[db][cb] = mfma16<BF16>(vf, pf[ks][cb], o[db][cb]);
       }
+    }
   };
 
   int stage = stage0;
