@@ -649,19 +649,27 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
       }
     }
 
+    // k-step outer: the two MFMAs into one accumulator are 8 * NCB apart
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      // one base per dim block; the block offsets fold into the instruction
-      const uint32_t vb = st + tl.v_lds[db];
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int db = 0; db < 8; ++db) {
+        // one base per dim block; the block offsets fold into the instruction
+        const uint32_t vb = st + tl.v_lds[db];
         const u32x2 lo = lds_read_tr16(vb + (4 + 2 * ks) * kTileBlock);
         const u32x2 hi = lds_read_tr16(vb + (5 + 2 * ks) * kTileBlock);
         const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) o[db][cb] = mfma16<BF16>(vf, pf[ks][cb], o[db][cb]);
       }
+    // V^T operand reads three blocks ahead of their MFMAs (LDS latency)
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 13; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NCB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 3 * NCB, 0);
   };
 
   int stage = stage0;
