@@ -19,6 +19,7 @@
 //    accumulation (chunked prefill, DFlash blocks, verify rows).
 //  * attn_merge_kernel: combines split-KV partials by their log-sum-exp, one
 //    wavefront per (query row, head) with a batch of splits in flight.
+#include <atomic>
 #include <type_traits>
 
 #include "attn_types.hpp"
@@ -864,16 +865,26 @@ int decode_wg_waves(int hkv) {
   return 1;
 }
 
+// Raises a kernel's dynamic LDS limit (the rings exceed the 64 KB default)
+// once per device; `done` holds one bit per device id.  Safe to call from
+// several host threads.
+static hipError_t allow_lds(const void* fn, size_t bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t(1) << dev : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess && bit != 0) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
+
 template <bool BF16, int WAVES, int NCB>
 static hipError_t decode_launch(const AttnArgs& a, int causal, int grid, hipStream_t st) {
   const size_t lds = (size_t)WAVES * dec_units<WAVES>() * kDecUnit + 16;
-  static bool lds_ok = false;  // the ring may exceed the 64 KB default
-  if (!lds_ok) {
-    const hipError_t e = hipFuncSetAttribute((const void*)attn_decode_kernel<BF16, WAVES, NCB>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    lds_ok = true;
-  }
+  static std::atomic<uint64_t> lds_ok{0};
+  const hipError_t e = allow_lds((const void*)attn_decode_kernel<BF16, WAVES, NCB>, lds, lds_ok);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((attn_decode_kernel<BF16, WAVES, NCB>), dim3(grid), dim3(64 * WAVES), lds, st, a, causal);
   return hipGetLastError();
 }
@@ -912,13 +923,9 @@ hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st)
 template <bool BF16, bool CAUSAL>
 static hipError_t tile_launch(const AttnArgs& a, int grid, hipStream_t st) {
   const size_t lds = 2 * kTileStage;
-  static bool lds_ok = false;
-  if (!lds_ok) {
-    const hipError_t e = hipFuncSetAttribute((const void*)attn_tile_kernel<BF16, CAUSAL>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    lds_ok = true;
-  }
+  static std::atomic<uint64_t> lds_ok{0};
+  const hipError_t e = allow_lds((const void*)attn_tile_kernel<BF16, CAUSAL>, lds, lds_ok);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((attn_tile_kernel<BF16, CAUSAL>), dim3(grid), dim3(256), lds, st, a);
   return hipGetLastError();
 }
