@@ -468,9 +468,13 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
           if (a.lse != nullptr && J == 0) a.lse[(size_t)crow[cb] * a.hq + chead[cb]] = l2 * kLn2;
         } else {
           const size_t pslot = (size_t)(w.part + (16 * cb + L) / G);
-          float* po = a.part_o + (pslot * a.hq + chead[cb]) * kHeadDim + 4 * J;
+          uint16_t* po = a.part_o + (pslot * a.hq + chead[cb]) * kHeadDim + 4 * J;
 #pragma unroll
-          for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db][cb] * inv;
+          for (int db = 0; db < 8; ++db) {
+            const u32x2 v = {pack2<BF16>(o[db][cb][0] * inv, o[db][cb][1] * inv),
+                             pack2<BF16>(o[db][cb][2] * inv, o[db][cb][3] * inv)};
+            *reinterpret_cast<u32x2*>(po + 16 * db) = v;
+          }
           if (J == 0) a.part_lse[pslot * a.hq + chead[cb]] = l2;
         }
       }
@@ -719,9 +723,13 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
           if (a.lse != nullptr && J == 0) a.lse[(size_t)crow[cb] * a.hq + chead[cb]] = l2 * kLn2;
         } else {
           const size_t slot = (size_t)(w.part + (n / G));
-          float* po = a.part_o + (slot * a.hq + chead[cb]) * kHeadDim + 4 * J;
+          uint16_t* po = a.part_o + (slot * a.hq + chead[cb]) * kHeadDim + 4 * J;
 #pragma unroll
-          for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db) = o[db][cb] * inv;
+          for (int db = 0; db < 8; ++db) {
+            const u32x2 v = {pack2<BF16>(o[db][cb][0] * inv, o[db][cb][1] * inv),
+                             pack2<BF16>(o[db][cb][2] * inv, o[db][cb][3] * inv)};
+            *reinterpret_cast<u32x2*>(po + 16 * db) = v;
+          }
           if (J == 0) a.part_lse[slot * a.hq + chead[cb]] = l2;
         }
       }
@@ -818,15 +826,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = 0; sp0 < mr.nsplit; sp0 += kMergeBatch) {
       float l[kMergeBatch];
-      f32x4 v[kMergeBatch];
+      u32x2 rv[kMergeBatch];  // four 16-bit partial values
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         l[u] = kNegInf;
-        v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        rv[u] = u32x2{0u, 0u};
         if (sp0 + u < mr.nsplit) {  // wave-uniform
           const size_t slot = (size_t)(mr.part + (sp0 + u) * mr.stride);
           l[u] = a.part_lse[slot * hq + hh];
-          v[u] = *reinterpret_cast<const f32x4*>(a.part_o + (slot * hq + hh) * kHeadDim + d);
+          rv[u] = *reinterpret_cast<const u32x2*>(a.part_o + (slot * hq + hh) * kHeadDim + d);
         }
       }
       float bm = m;
@@ -839,8 +847,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         const float wt = fast_exp2(l[u] - mu);
+        const f32x4 v = {lo_f32<BF16>(rv[u][0]), hi_f32<BF16>(rv[u][0]), lo_f32<BF16>(rv[u][1]),
+                         hi_f32<BF16>(rv[u][1])};
         wsum += wt;
-        acc += wt * v[u];
+        acc += wt * v;
       }
       m = bm;
     }

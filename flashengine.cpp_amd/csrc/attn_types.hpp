@@ -96,7 +96,7 @@ struct AttnArgs {
   const DecodeItem* ditems;  // decode only: the pieces, share by share
   const ShareStart* shares;  // decode only: one record per share
   int n_share_cap;           // decode only: records in `shares`
-  float* part_o;           // [slots][hq][128] fp32, normalised per split
+  uint16_t* part_o;        // [slots][hq][128] in the attention's 16-bit type, normalised per split
   float* part_lse;         // [slots][hq] log2 domain
   int hq;
   int hkv;
@@ -111,7 +111,7 @@ struct MergeArgs {
   const MergeRow* rows;
   const int32_t* n_rows;
   int rows_cap;            // entries of `rows`
-  const float* part_o;
+  const uint16_t* part_o;
   const float* part_lse;
   int hq;
 };

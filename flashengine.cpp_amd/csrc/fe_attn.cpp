@@ -100,7 +100,9 @@ Layout make_layout(const PlanShape& sh) {
 // counts[] indices
 enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
 
-constexpr size_t kPartialBytes = 64u << 20;  // split-KV workspace (fp32 partial rows)
+// Split-KV slot budget: as many (row, all heads) partial slots as 64 MiB of
+// fp32 rows would hold; the rows are stored in 16 bits, so they take half.
+constexpr size_t kPartialBytes = 64u << 20;
 
 }  // namespace
 
@@ -116,7 +118,7 @@ struct fe_attn_plan {
   Layout lay{};
   uint8_t* dev = nullptr;      // metadata arena
   uint8_t* host = nullptr;     // pinned mirror
-  float* part_o = nullptr;
+  uint16_t* part_o = nullptr;  // 16-bit partial rows
   float* part_lse = nullptr;
   hipEvent_t staged = nullptr;
   bool staged_pending = false;
@@ -182,7 +184,7 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (hipHostMalloc(&p->host, p->lay.total, hipHostMallocDefault) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipHostMalloc(plan staging) failed");
   std::memset(p->host, 0, p->lay.total);
-  if (hipMalloc(&p->part_o, (size_t)sh.partial_cap * hq * kHeadDim * sizeof(float)) != hipSuccess)
+  if (hipMalloc(&p->part_o, (size_t)sh.partial_cap * hq * kHeadDim * sizeof(uint16_t)) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipMalloc(split-KV partials) failed");
   if (hipMalloc(&p->part_lse, (size_t)sh.partial_cap * hq * sizeof(float)) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipMalloc(split-KV lse) failed");
