@@ -375,9 +375,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
 
     for (int tok = t0; tok < t1; tok += 16) {
       // The workgroup's wavefronts (consecutive kv heads of one share, the
-      // same blocks in the same order) stay in step, so each page is
-      // requested by all of them at once.
-      __builtin_amdgcn_s_barrier();
+      // same blocks in the same order) are brought back in step every four
+      // blocks, so each page is requested by all of them at about the same
+      // time (every block: 0.3 % slower; never: 0.8 % slower).
+      if (((tok - t0) & 48) == 0) __builtin_amdgcn_s_barrier();
       refill();
       wait_units<U>(issued - consumed - 2);
       const uint32_t kst = ring + (uint32_t)(r_slot * kDecUnit);
