@@ -193,3 +193,32 @@ def test_graph_keeps_captured_decode_variant(dev):
     with pytest.raises(RuntimeError):
         narrow.prepare(verify.qo, verify.kv, verify.pages, verify.last, verify.batch, verify.rows, graph=True)
     narrow.close()
+
+
+def test_two_plans_on_two_streams(dev):
+    """Two plans (a decode batch and a prefill batch, different shapes) are
+    prepared and run on two streams at once, three times in a row; both
+    results match the oracle.  Plans share no state, so streams may run
+    them concurrently."""
+    dec = W.make_batch(32, 8, starts=[3000, 40, 700, 1500], qlens=[1, 1, 1, 1], seed=21, extra_pages=1)
+    pre = W.make_batch(16, 4, starts=[0, 300], qlens=[200, 90], seed=22, extra_pages=1)
+    jobs = []
+    for b, causal, seed in ((dec, True, 21), (pre, True, 22)):
+        q, kc, vc = W.make_tensors(b, seed=seed)
+        plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
+        want = A.run(b, q, kc, vc, causal)
+        jobs.append(dict(b=b, plan=plan, causal=causal, want=want, q=q.to(dev), kc=kc.to(dev), vc=vc.to(dev),
+                         out=torch.zeros(b.rows, b.hq, 128, dtype=torch.bfloat16, device=dev),
+                         lse=torch.zeros(b.rows, b.hq, device=dev), st=torch.cuda.Stream()))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for j in jobs:
+            b = j["b"]
+            with torch.cuda.stream(j["st"]):
+                j["out"].zero_()
+                j["plan"].prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows, stream=j["st"])
+                j["plan"].run(j["q"], j["kc"], j["vc"], j["out"], causal=j["causal"], lse=j["lse"], stream=j["st"])
+    torch.cuda.synchronize()
+    for j in jobs:
+        check(j["out"].cpu(), j["lse"].cpu(), *j["want"])
+        j["plan"].close()
