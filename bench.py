@@ -116,7 +116,7 @@ def decode_headline(steps, warmup, dev):
 
 def secondary(dev, only=None):
     """Other workload shapes: ms per call and throughput.  `only` selects one
-    of prefill / dflash / mixed / long."""
+    of prefill / dflash / mixed / long / graph."""
     import torch
 
     import feattn
@@ -137,6 +137,8 @@ def secondary(dev, only=None):
         _mixed(dev, res)
     if want("long"):
         _long(dev, res)
+    if want("graph"):
+        _graph(dev, res)
     return res
 
 
@@ -226,6 +228,47 @@ def _mixed(dev, res):
     log("mixed", res["mixed_qwen3_30b"])
 
 
+def _graph(dev, res):
+    import torch
+
+    import feattn
+    from feattn import workloads as W
+
+    # the headline decode batch as the engine runs decode steps: the plan
+    # prepared in graph mode outside capture, the attention calls of a step
+    # (one per layer; here 8 layers over 4 KV pools) captured in one HIP
+    # graph and replayed (src/cuda_model.cpp:150-157); ms is per call
+    layers = 8
+    b = W.qwen3_8b_decode()
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows, graph=True)
+    pools = make_pools(b, 4, dev, torch.bfloat16)
+    q = torch.randn(b.rows, b.hq, 128, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    lse = torch.empty(b.rows, b.hq, device=dev)
+
+    def step():
+        for i in range(layers):
+            kc, vc = pools[i % len(pools)]
+            plan.run(q, kc, vc, out, causal=True, lse=lse)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    ms = event_time_ms(lambda i: graph.replay(), 20, 3) / layers
+    res["decode_graph_replay"] = {"workload": "headline decode batch, 8 attention calls per captured graph",
+                                  "ms": round(ms, 4), "gbs": round(W.decode_bytes(b) / ms / 1e6, 1)}
+    log("graph", res["decode_graph_replay"])
+    del graph
+    plan.close()
+
+
 def _long(dev, res):
     import torch
 
@@ -295,7 +338,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long"],
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph"],
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -127,6 +127,7 @@ struct fe_attn_plan {
   bool prepared = false;
   bool graph = false;
   int graph_nc = 0;
+  int graph_tile = -1;  // the first graph prepare had tile work (1) or not (0)
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;  // wavefronts per decode workgroup
@@ -225,6 +226,13 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     if (nc > p->graph_nc)
       return fail(FE_EINVAL, "graph plan layout changed: decode rows per sequence grew after capture");
     nc = p->graph_nc;
+    // Likewise whether the tile kernel is launched at all: a graph of
+    // decode-only steps carries no tile launch, and a later prepare may not
+    // bring tile work to it.
+    const int tile = bp.mode[0].tile.empty() && bp.mode[1].tile.empty() ? 0 : 1;
+    if (p->graph_tile < 0) p->graph_tile = tile;
+    if (tile > p->graph_tile)
+      return fail(FE_EINVAL, "graph plan layout changed: multi-row tile work after a capture without it");
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   // The pinned mirror may still be read by the previous prepare's copies.
@@ -333,7 +341,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     e = launch_decode(d, p->bf16, p->decode_wg, p->decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
-  if (p->graph || p->n_tile[mode] > 0) {
+  if (p->graph ? p->graph_tile > 0 : p->n_tile[mode] > 0) {
     AttnArgs t = a;
     t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.tile[mode]);
     t.n_items = counts + (mode ? kCntTile1 : kCntTile0);

@@ -144,10 +144,10 @@ def test_many_columns_per_kv_head(dev, hq, hkv, starts, qlens, causal):
 
 def test_graph_keeps_captured_decode_variant(dev):
     """A graph captured on 8-row verify items (32 columns per kv head: the
-    two-block decode variant) replays single rows and 16-row blocks (tile
-    items) correctly; a graph captured on single rows refuses 8-row items
-    afterwards (reference refusal of layout changes:
-    src/flashinfer_attention.cu:32)."""
+    two-block decode variant) replays single rows correctly and refuses
+    16-row blocks (tile work, which the captured decode-only step does not
+    launch); a graph captured on single rows refuses 8-row items afterwards
+    (reference refusal of layout changes: src/flashinfer_attention.cu:32)."""
     hq, hkv, blocks = 32, 8, 700
     kc = torch.zeros(blocks + 1, 16, hkv, 128, dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
@@ -176,15 +176,17 @@ def test_graph_keeps_captured_decode_variant(dev):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         plan.run(q, kc, vc, out, causal=True, lse=lse)
-    steps = [W.make_batch(hq, hkv, starts=[3000, 5, 700, 1800], qlens=[1] * 4, seed=2, pool=blocks),
-             W.make_batch(hq, hkv, starts=[300, 1500, 60, 2500], qlens=[16] * 4, seed=3, pool=blocks),
-             verify]
+    steps = [W.make_batch(hq, hkv, starts=[3000, 5, 700, 1800], qlens=[1] * 4, seed=2, pool=blocks), verify]
     for seed, bb in enumerate(steps, start=2):
         qq, kk, vv = load(bb, seed)
         graph.replay()
         torch.cuda.synchronize()
         want_out, want_lse = A.run(bb, qq, kk, vv, True)
         check(out[:bb.rows].cpu(), lse[:bb.rows].cpu(), want_out, want_lse)
+    blocks16 = W.make_batch(hq, hkv, starts=[300, 1500, 60, 2500], qlens=[16] * 4, seed=3, pool=blocks)
+    with pytest.raises(RuntimeError):
+        plan.prepare(blocks16.qo, blocks16.kv, blocks16.pages, blocks16.last, blocks16.batch, blocks16.rows,
+                     graph=True)
     plan.close()
 
     narrow = feattn.Plan(hq, hkv, 128, 16, 4, 200, True, blocks)
