@@ -5,6 +5,7 @@ per-step metadata builder (src/cuda_model.cpp:131-142) bit for bit, graph
 padding and error cases included."""
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -217,3 +218,16 @@ def test_rope_table_rejects_bad_arguments():
         assert b"rope table" in lib.fe_attn_last_error()
     assert lib.fe_rope_table(None, 16, 128, 1e6, None) == feattn.FE_EINVAL
     assert b"null" in lib.fe_attn_last_error()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message before
+    touching a device."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode != 0
+    assert "one GPU" in (res.stdout + res.stderr)
