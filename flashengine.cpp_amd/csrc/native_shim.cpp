@@ -1,6 +1,7 @@
 // fe::cuda:: entry points over the C ABI: status codes become
 // std::runtime_error, matching the reference's check() behaviour
 // (src/flashinfer_attention.cu:13, src/cuda_kernels.cu:10).
+#include <new>
 #include <stdexcept>
 #include <string>
 
@@ -23,7 +24,12 @@ void check(int rc) {
 AttentionPlan* create_plan(int hq, int hkv, int dim, int page, int max_batch, int max_pages, bool bf16, int blocks) {
   fe_attn_plan* p = nullptr;
   check(fe_attn_plan_create(hq, hkv, dim, page, max_batch, max_pages, bf16 ? 1 : 0, blocks, &p));
-  return new AttentionPlan{p};
+  auto* handle = new (std::nothrow) AttentionPlan{p};
+  if (handle == nullptr) {
+    fe_attn_plan_destroy(p);
+    throw std::bad_alloc();
+  }
+  return handle;
 }
 
 void destroy_plan(AttentionPlan* plan) {
