@@ -5,6 +5,8 @@
 
 #include <algorithm>
 #include <deque>
+#include <memory>
+#include <new>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -41,15 +43,19 @@ struct fe_blocks {
 };
 
 extern "C" int fe_blocks_create(int64_t total, int64_t block_size, fe_blocks** out) {
-  if (out == nullptr) return report_error(FE_EINVAL, "out is null");
-  *out = nullptr;
-  if (total <= 0 || total >= INT32_MAX || block_size <= 0) return report_error(FE_EINVAL, "invalid KV page pool");
-  auto* b = new fe_blocks();
-  b->block_size = block_size;
-  b->used.assign((size_t)total, 0);
-  for (int32_t i = 0; i < (int32_t)total; ++i) b->free.push_back(i);
-  *out = b;
-  return FE_OK;
+  try {
+    if (out == nullptr) return report_error(FE_EINVAL, "out is null");
+    *out = nullptr;
+    if (total <= 0 || total >= INT32_MAX || block_size <= 0) return report_error(FE_EINVAL, "invalid KV page pool");
+    std::unique_ptr<fe_blocks> b(new fe_blocks());
+    b->block_size = block_size;
+    b->used.assign((size_t)total, 0);
+    for (int32_t i = 0; i < (int32_t)total; ++i) b->free.push_back(i);
+    *out = b.release();
+    return FE_OK;
+  } catch (const std::bad_alloc&) {
+    return report_error(FE_ENOMEM, "out of host memory");
+  }
 }
 
 extern "C" int fe_blocks_destroy(fe_blocks* b) {
@@ -58,40 +64,48 @@ extern "C" int fe_blocks_destroy(fe_blocks* b) {
 }
 
 extern "C" int fe_blocks_ensure(fe_blocks* b, int64_t seq, int64_t target, int* ok_out) {
-  if (b == nullptr || ok_out == nullptr) return report_error(FE_EINVAL, "null argument");
-  if (target < 0) return report_error(FE_EINVAL, "negative token target");
-  std::vector<int32_t>& t = b->tables[seq];
-  const size_t needed = (size_t)((target + b->block_size - 1) / b->block_size);
-  *ok_out = 1;
-  if (needed <= t.size()) return FE_OK;
-  if (needed - t.size() > b->free.size()) {  // all or nothing
-    *ok_out = 0;
-    if (t.empty()) b->tables.erase(seq);
+  try {
+    if (b == nullptr || ok_out == nullptr) return report_error(FE_EINVAL, "null argument");
+    if (target < 0) return report_error(FE_EINVAL, "negative token target");
+    std::vector<int32_t>& t = b->tables[seq];
+    const size_t needed = (size_t)((target + b->block_size - 1) / b->block_size);
+    *ok_out = 1;
+    if (needed <= t.size()) return FE_OK;
+    if (needed - t.size() > b->free.size()) {  // all or nothing
+      *ok_out = 0;
+      if (t.empty()) b->tables.erase(seq);
+      return FE_OK;
+    }
+    while (t.size() < needed) {
+      const int32_t id = b->free.front();
+      b->free.pop_front();
+      if (b->used[id]) return report_error(FE_EINVAL, "KV page allocated twice");
+      b->used[id] = 1;
+      ++b->n_used;
+      t.push_back(id);
+    }
     return FE_OK;
+  } catch (const std::bad_alloc&) {
+    return report_error(FE_ENOMEM, "out of host memory");
   }
-  while (t.size() < needed) {
-    const int32_t id = b->free.front();
-    b->free.pop_front();
-    if (b->used[id]) return report_error(FE_EINVAL, "KV page allocated twice");
-    b->used[id] = 1;
-    ++b->n_used;
-    t.push_back(id);
-  }
-  return FE_OK;
 }
 
 extern "C" int fe_blocks_release(fe_blocks* b, int64_t seq) {
-  if (b == nullptr) return report_error(FE_EINVAL, "null argument");
-  auto it = b->tables.find(seq);
-  if (it == b->tables.end()) return FE_OK;
-  for (int32_t id : it->second) {
-    if (!b->used[id]) return report_error(FE_EINVAL, "KV page released twice");
-    b->used[id] = 0;
-    --b->n_used;
-    b->free.push_back(id);
+  try {
+    if (b == nullptr) return report_error(FE_EINVAL, "null argument");
+    auto it = b->tables.find(seq);
+    if (it == b->tables.end()) return FE_OK;
+    for (int32_t id : it->second) {
+      if (!b->used[id]) return report_error(FE_EINVAL, "KV page released twice");
+      b->used[id] = 0;
+      --b->n_used;
+      b->free.push_back(id);
+    }
+    b->tables.erase(it);
+    return FE_OK;
+  } catch (const std::bad_alloc&) {
+    return report_error(FE_ENOMEM, "out of host memory");
   }
-  b->tables.erase(it);
-  return FE_OK;
 }
 
 extern "C" int fe_blocks_table(const fe_blocks* b, int64_t seq, int32_t* out, int cap, int* n_out) {

@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <new>
 #include <string>
 
 #include "attn_types.hpp"
@@ -168,7 +169,8 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
 
   sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
   sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
-  auto* p = new fe_attn_plan();
+  auto* p = new (std::nothrow) fe_attn_plan();
+  if (p == nullptr) return fail(FE_ENOMEM, "out of host memory");
   p->sh = sh;
   p->bf16 = bf16 != 0;
   p->device = dev;

@@ -4,6 +4,7 @@
 #include "planner.hpp"
 
 #include <algorithm>
+#include <new>
 
 #include "fe_attn.h"
 
@@ -88,7 +89,7 @@ int validate_shape(const PlanShape& sh, std::string& err) {
   return FE_OK;
 }
 
-int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,
                const int32_t* last, int batch, int rows, BuiltPlan& out, std::string& err) {
   int rc = validate_shape(sh, err);
   if (rc != FE_OK) return rc;
@@ -330,4 +331,15 @@ int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const 
   return FE_OK;
 }
 
+int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+               const int32_t* last, int batch, int rows, BuiltPlan& out, std::string& err) {
+  try {
+    return build_plan_impl(sh, qo, kv, pages, last, batch, rows, out, err);
+  } catch (const std::bad_alloc&) {
+    err = "out of host memory while building the work lists";
+    return FE_ENOMEM;
+  }
+}
+
 }  // namespace feattn
+
