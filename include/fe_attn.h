@@ -45,7 +45,7 @@ enum {
   FE_EINVAL = -1,    /* bad argument or metadata (reference: std::runtime_error) */
   FE_ECAPACITY = -2, /* metadata exceeds the capacity fixed at create time */
   FE_EDEVICE = -3,   /* HIP runtime error */
-  FE_ENOMEM = -4     /* device or pinned allocation failed */
+  FE_ENOMEM = -4     /* device, pinned or host allocation failed */
 };
 
 typedef struct fe_attn_plan fe_attn_plan;
