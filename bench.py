@@ -375,7 +375,8 @@ def main():
         "config": {"workload": "Qwen3-8B-shape paged decode attention: 64 seqs, ctx U[512,4096] "
                                "(seeded), hq 32 / hkv 8 / d 128, 16-token pages, bf16, 4 rotated "
                                "KV pools",
-                   "batch": b.batch, "context_tokens": sum(b.lens), "pages": b.blocks},
+                   "batch": b.batch, "context_tokens": sum(b.lens), "pages": b.blocks,
+                   "seeds": {"lengths_and_pages": 2, "kv_pools": 1234}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
