@@ -68,10 +68,15 @@ def event_time_ms(fn, iters, warmup):
     return start.elapsed_time(end) / iters
 
 
+DECODE_SEED = 2   # context lengths and page permutation of the headline decode batch
+POOL_SEED = 1234  # K/V cache contents
+Q_SEED = 4321     # query rows
+
+
 def make_pools(b, n, dev, dtype):
     import torch
 
-    g = torch.Generator(device=dev).manual_seed(1234)
+    g = torch.Generator(device=dev).manual_seed(POOL_SEED)
     shape = (b.blocks + 1, b.page, b.hkv, 128)
     pools = []
     for _ in range(n):
@@ -90,7 +95,8 @@ def attn_setup(b, dev, dtype, causal, npools):
                        b.blocks)
     plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
     pools = make_pools(b, npools, dev, dtype)
-    q = torch.randn(b.rows, b.hq, 128, device=dev).to(dtype)
+    gq = torch.Generator(device=dev).manual_seed(Q_SEED)
+    q = torch.randn(b.rows, b.hq, 128, generator=gq, device=dev).to(dtype)
     out = torch.empty_like(q)
     lse = torch.empty(b.rows, b.hq, device=dev)
 
@@ -106,7 +112,7 @@ def decode_headline(steps, warmup, dev):
 
     from feattn import workloads as W
 
-    b = W.qwen3_8b_decode()
+    b = W.qwen3_8b_decode(seed=DECODE_SEED)
     plan, step = attn_setup(b, dev, torch.bfloat16, True, 4)
     ms = event_time_ms(step, steps, warmup)
     nbytes = W.decode_bytes(b)
@@ -376,7 +382,7 @@ def main():
                                "(seeded), hq 32 / hkv 8 / d 128, 16-token pages, bf16, 4 rotated "
                                "KV pools",
                    "batch": b.batch, "context_tokens": sum(b.lens), "pages": b.blocks,
-                   "seeds": {"lengths_and_pages": 2, "kv_pools": 1234}},
+                   "seeds": {"lengths_and_pages": DECODE_SEED, "kv_pools": POOL_SEED, "q": Q_SEED}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
