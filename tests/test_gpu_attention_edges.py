@@ -2,7 +2,9 @@
 16, page-boundary lengths (len 1, len = page, len = page + 1, a chunk with no
 prefix), an empty batch, stale or poisoned cache slots outside every visible
 range (they must not leak into results: the reference kernel reads only
-visible tokens), and plan capacity limits.  Tolerance as in
+visible tokens), plan capacity limits, and scores far outside the range of
+an exponential (a dominant first token, scores rising or falling by ~10 in
+log2 units every 48 tokens, natural-log LSE up to ~300).  Tolerance as in
 test_gpu_attention.py: |a-b| <= 1e-2 + 1e-2*|b|, LSE within 1e-3."""
 
 import math
@@ -224,3 +226,44 @@ def test_two_plans_on_two_streams(dev):
     for j in jobs:
         check(j["out"].cpu(), j["lse"].cpu(), *j["want"])
         j["plan"].close()
+
+
+def _extreme_scores(b, pattern, dtype, seed):
+    """Positive q and k in [0.5, 1), k scaled by a function of the token's
+    logical position, so that every score is positive and its size is set by
+    the position: "rising" steps up by ~10 (log2 units) every 48 tokens,
+    "falling" steps down (both capped at 40x, which keeps the fp32 sums of
+    the scores exact to ~1e-4), "sink" puts token 0 ~480x above the rest."""
+    _, _, vc = W.make_tensors(b, seed=seed, dtype=dtype)
+    g = torch.Generator().manual_seed(seed + 99)
+    q = torch.rand((b.rows, b.hq, 128), generator=g) * 0.5 + 0.5
+    k = torch.rand(vc.shape, generator=g) * 0.5 + 0.5
+    pos = torch.zeros(vc.shape[0], vc.shape[1])
+    for s in range(b.batch):
+        for t in range(b.lens[s]):
+            pos[b.tables[s][t // b.page], t % b.page] = t
+    pos = pos.view(vc.shape[0], vc.shape[1], 1, 1)
+    if pattern == "rising":
+        scale = (1.0 + torch.floor(pos / 48)).clamp(max=40.0)
+    elif pattern == "falling":
+        scale = (1.0 + torch.floor((pos.max() - pos) / 48)).clamp(max=40.0)
+    else:
+        scale = torch.where(pos == 0, torch.tensor(24.0), torch.tensor(0.05))
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    return q.to(dt), (k * scale).to(dt), vc
+
+
+@pytest.mark.parametrize("pattern", ["rising", "falling", "sink"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_extreme_scores(dev, pattern, causal, dtype):
+    """Decode rows, a 200-row chunk, a 16-row block and a split long context
+    whose scores exceed the exponential's range by far: the running maximum
+    must be raised (with l and o rescaled) as often and as far as the scores
+    demand, and tokens far below it must not disturb the result."""
+    b = W.make_batch(32, 8, starts=[2000, 0, 700, 30, 20000], qlens=[1, 200, 16, 1, 1], seed=5)
+    q, kc, vc = _extreme_scores(b, pattern, dtype, seed=7)
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    assert float(want_lse.max()) > 150.0  # far past exp's range without the maximum taken out
+    out, lse = run(b, q, kc, vc, causal, dev)
+    check(out, lse, want_out, want_lse)
