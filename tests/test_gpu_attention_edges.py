@@ -199,6 +199,70 @@ def test_graph_keeps_captured_decode_variant(dev):
     narrow.close()
 
 
+@pytest.mark.parametrize("hq,hkv,qlen", [(32, 8, 16), (32, 8, 11), (32, 4, 8), (64, 8, 8)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_block_items_vs_oracle(dev, hq, hkv, qlen, causal, dtype):
+    """33..64-column items (16-row DFlash blocks, 8-row items with 8 heads per
+    kv head) beside single rows, over a split 20000-token context, a block
+    that is its whole context and short ones."""
+    b = W.make_batch(hq, hkv, starts=[20000, 3000, 16, 700, 0], qlens=[qlen, qlen, qlen, 1, qlen],
+                     seed=qlen + hkv, extra_pages=1)
+    q, kc, vc = W.make_tensors(b, seed=qlen, dtype=dtype)
+    out, lse = run(b, q, kc, vc, causal, dev)
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    check(out, lse, want_out, want_lse)
+
+
+def test_graph_captured_on_blocks(dev):
+    """A graph captured on 16-row blocks (tile work, no decode rows) replays
+    other block batches and single-row batches, each matching the oracle,
+    and refuses 8-row items, which need the wider decode variant than the
+    one captured (reference refusal of layout changes:
+    src/flashinfer_attention.cu:32)."""
+    hq, hkv, blocks = 32, 8, 900
+    kc = torch.zeros(blocks + 1, 16, hkv, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = torch.zeros(64, hq, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros_like(q)
+    lse = torch.zeros(64, hq, device=dev)
+    plan = feattn.Plan(hq, hkv, 128, 16, 4, 250, True, blocks)
+
+    def load(bb, seed):
+        qq, kk, vv = W.make_tensors(bb, seed=seed)
+        kc.copy_(kk.to(dev))
+        vc.copy_(vv.to(dev))
+        q.zero_()
+        q[:bb.rows].copy_(qq.to(dev))
+        plan.prepare(bb.qo, bb.kv, bb.pages, bb.last, bb.batch, bb.rows, graph=True)
+        return qq, kk, vv
+
+    first = W.make_batch(hq, hkv, starts=[900, 2000, 40, 1200], qlens=[16] * 4, seed=1, pool=blocks)
+    load(first, 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.run(q, kc, vc, out, causal=False, lse=lse)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(q, kc, vc, out, causal=False, lse=lse)
+    steps = [first,
+             W.make_batch(hq, hkv, starts=[3500, 5, 700, 1800], qlens=[16] * 4, seed=2, pool=blocks),
+             W.make_batch(hq, hkv, starts=[3000, 5, 700, 1800], qlens=[1] * 4, seed=3, pool=blocks)]
+    for seed, bb in enumerate(steps, start=1):
+        qq, kk, vv = load(bb, seed)
+        graph.replay()
+        torch.cuda.synchronize()
+        want_out, want_lse = A.run(bb, qq, kk, vv, False)
+        check(out[:bb.rows].cpu(), lse[:bb.rows].cpu(), want_out, want_lse)
+    eight = W.make_batch(hq, hkv, starts=[100, 2500, 60], qlens=[8, 8, 8], seed=4, pool=blocks)
+    with pytest.raises(RuntimeError):
+        plan.prepare(eight.qo, eight.kv, eight.pages, eight.last, eight.batch, eight.rows, graph=True)
+    plan.close()
+
+
 def test_two_plans_on_two_streams(dev):
     """Two plans (a decode batch and a prefill batch, different shapes) are
     prepared and run on two streams at once, three times in a row; both
