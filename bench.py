@@ -1,6 +1,6 @@
 """Benchmark of the MI355X paged-KV attention path.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 
 Headline workload (one step = one paged decode attention call over the
 whole batch, inputs resident in HBM): Qwen3-8B head layout (32 q / 8 kv
