@@ -311,6 +311,13 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
   if (!p->prepared) return fail(FE_EINVAL, "attention called before prepare_plan");
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
     return fail(FE_EINVAL, "null tensor pointer");
+  // The kernels move q rows and K/V cache rows in 16-byte pieces (direct
+  // to LDS) and write 8-byte pieces of out.
+  const void* rows16[] = {q, k_cache, v_cache, out};
+  for (const void* ptr : rows16)
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+      return fail(FE_EINVAL, "attention: q, k_cache, v_cache and out must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(lse) % 4 != 0) return fail(FE_EINVAL, "attention: lse must be 4-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mode = causal ? 1 : 0;
   const int32_t* counts = reinterpret_cast<const int32_t*>(p->dev + p->lay.counts);

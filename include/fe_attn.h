@@ -80,7 +80,9 @@ int fe_attn_plan_prepare(fe_attn_plan* plan, const int32_t* qo,
  * out[r,h,:] = softmax_t(q[r,h].K[t,h/(hq/hkv)] / sqrt(dim) + mask) . V.
  * `lse` (may be NULL; the reference has no such output) receives
  * [rows][hq] fp32 natural-log log-sum-exp of the scaled logits over the
- * visible keys.  causal = 0 is DFlash's non-causal block attention. */
+ * visible keys.  causal = 0 is DFlash's non-causal block attention.
+ * q, k_cache, v_cache and out must be 16-byte aligned (FE_EINVAL otherwise),
+ * as the contiguous tensors of a caching allocator are. */
 int fe_attn_run(fe_attn_plan* plan, const void* q, const void* k_cache,
                 const void* v_cache, void* out, float* lse, int causal,
                 void* stream);

@@ -263,6 +263,31 @@ def test_graph_captured_on_blocks(dev):
     plan.close()
 
 
+def test_misaligned_tensors_are_refused(dev):
+    """q, the K/V caches and out move in 16-byte pieces: a view starting 8
+    bytes into its storage is refused before any launch, and the aligned
+    call that follows still matches the oracle."""
+    b = W.make_batch(32, 8, starts=[100, 40], qlens=[1, 3], seed=31)
+    q, kc, vc = W.make_tensors(b, seed=31)
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    out = torch.zeros_like(qd)
+    n = qd.numel()
+    shifted = torch.zeros(n + 8, dtype=qd.dtype, device=dev)[4:4 + n].view_as(qd)
+    shifted.copy_(qd)
+    with pytest.raises(RuntimeError, match="aligned"):
+        plan.run(shifted, kd, vd, out, causal=True)
+    with pytest.raises(RuntimeError, match="aligned"):
+        plan.run(qd, kd, vd, torch.zeros(n + 8, dtype=qd.dtype, device=dev)[4:4 + n].view_as(qd), causal=True)
+    lse = torch.zeros(b.rows, b.hq, device=dev)
+    plan.run(qd, kd, vd, out, causal=True, lse=lse)
+    torch.cuda.synchronize()
+    plan.close()
+    want_out, want_lse = A.run(b, q, kc, vc, True)
+    check(out.cpu(), lse.cpu(), want_out, want_lse)
+
+
 def test_two_plans_on_two_streams(dev):
     """Two plans (a decode batch and a prefill batch, different shapes) are
     prepared and run on two streams at once, three times in a row; both
