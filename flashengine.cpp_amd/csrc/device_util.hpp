@@ -57,6 +57,38 @@ __device__ __forceinline__ uint32_t from_f32_rne(float f) {
   }
 }
 
+// Eight fp32 values -> four packed 16-bit pairs (out[i] = v[2i] | v[2i+1] <<
+// 16), bit-identical to from_f32_rne on every element.  bf16: the hardware
+// converter (v_cvt_pk_bf16_f32, round to nearest even, one instruction per
+// pair) gives the same bits for every non-NaN input; it would keep NaN
+// payload bits, so a lane holding a NaN redoes its packing with
+// from_f32_rne (0x7fc0).  fp16: from_f32_rne per element.
+template <bool BF16>
+__device__ __forceinline__ u32x4 pack8_rne(const float (&v)[8]) {
+  u32x4 out;
+  if constexpr (BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = v[2 * i], b = v[2 * i + 1];
+      asm("" : "+v"(a));  // the rounded fp32 values, not a folded product
+      asm("" : "+v"(b));
+      nan = nan || __builtin_isnan(a) || __builtin_isnan(b);
+      out[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    }
+    if (nan) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = from_f32_rne<true>(v[2 * i]) | (from_f32_rne<true>(v[2 * i + 1]) << 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = from_f32_rne<false>(v[2 * i]) | (from_f32_rne<false>(v[2 * i + 1]) << 16);
+  }
+  return out;
+}
+
 // Two fp32 -> packed 16-bit pair using the hardware converter (RNE); used for
 // softmax probabilities and attention outputs, where the tolerance, not bit
 // identity, is the contract.

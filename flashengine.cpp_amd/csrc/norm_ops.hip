@@ -102,18 +102,16 @@ __device__ __forceinline__ void normalize_head(u32x4& x, u32x4& y, u32x4 wl, u32
   for (int e = 0; e < 2; ++e) s[e] = __fadd_rn(s[e], s[e + 2]);                     // step 2
   const float total = __fadd_rn(s[0], s[1]);                                         // step 1
   const float scale = rsqrt_rn(__fadd_rn(__fdiv_rn(total, 128.f), eps));
-  u32x4 rx, ry;
+  float na[8], nb[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float w0 = lo_f32<BF16>(wl[i]), w1 = hi_f32<BF16>(wl[i]);
-    const float u0 = lo_f32<BF16>(wh[i]), u1 = hi_f32<BF16>(wh[i]);
-    rx[i] = from_f32_rne<BF16>(__fmul_rn(__fmul_rn(a[2 * i], scale), w0)) |
-            (from_f32_rne<BF16>(__fmul_rn(__fmul_rn(a[2 * i + 1], scale), w1)) << 16);
-    ry[i] = from_f32_rne<BF16>(__fmul_rn(__fmul_rn(b[2 * i], scale), u0)) |
-            (from_f32_rne<BF16>(__fmul_rn(__fmul_rn(b[2 * i + 1], scale), u1)) << 16);
+    na[2 * i] = __fmul_rn(__fmul_rn(a[2 * i], scale), lo_f32<BF16>(wl[i]));
+    na[2 * i + 1] = __fmul_rn(__fmul_rn(a[2 * i + 1], scale), hi_f32<BF16>(wl[i]));
+    nb[2 * i] = __fmul_rn(__fmul_rn(b[2 * i], scale), lo_f32<BF16>(wh[i]));
+    nb[2 * i + 1] = __fmul_rn(__fmul_rn(b[2 * i + 1], scale), hi_f32<BF16>(wh[i]));
   }
-  x = rx;
-  y = ry;
+  x = pack8_rne<BF16>(na);
+  y = pack8_rne<BF16>(nb);
 }
 
 // Work unit = (row, head in [0, hq + 2 hkv)): query heads are normalized with

@@ -21,25 +21,20 @@ __device__ __forceinline__ void rotate8(u32x4& x, u32x4& y, const float* cs, con
   const f32x4 s1 = reinterpret_cast<const f32x4*>(sn)[1];
   const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-  u32x4 rx, ry;
+  float na[8], nb[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t ox = 0, oy = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int e = 2 * i + h;
       const float a = h ? hi_f32<BF16>(x[i]) : lo_f32<BF16>(x[i]);
       const float b = h ? hi_f32<BF16>(y[i]) : lo_f32<BF16>(y[i]);
-      const float na = __fsub_rn(__fmul_rn(a, c[e]), __fmul_rn(b, s[e]));
-      const float nb = __fadd_rn(__fmul_rn(b, c[e]), __fmul_rn(a, s[e]));
-      ox |= from_f32_rne<BF16>(na) << (16 * h);
-      oy |= from_f32_rne<BF16>(nb) << (16 * h);
+      na[e] = __fsub_rn(__fmul_rn(a, c[e]), __fmul_rn(b, s[e]));
+      nb[e] = __fadd_rn(__fmul_rn(b, c[e]), __fmul_rn(a, s[e]));
     }
-    rx[i] = ox;
-    ry[i] = oy;
   }
-  x = rx;
-  y = ry;
+  x = pack8_rne<BF16>(na);
+  y = pack8_rne<BF16>(nb);
 }
 
 }  // namespace feattn

@@ -86,6 +86,33 @@ def test_norm_rope_append_vs_oracle(dev, bf16, rows, hq, hkv, extra):
     assert np.array_equal(u16(vcd).reshape(cs, -1), wvc)
 
 
+def test_norm_rope_append_special_values(dev):
+    """bf16 projection rows holding NaNs (several payloads), infinities,
+    the largest finite values and subnormals: every head, rotated or not,
+    matches the oracle bit for bit (a NaN or infinity poisons its head's
+    sum of squares; NaN results round to 0x7fc0)."""
+    rows, hq, hkv = 47, 32, 8
+    row_stride = (hq + 2 * hkv) * 128
+    buf, qw, kw, kc, vc, pos, slots, table, cs = make_fused_case(True, rows, hq, hkv, row_stride, 11)
+    specials = [0x7FC0, 0x7FC1, 0x7F81, 0xFFC0, 0x7FFF, 0x7F80, 0xFF80, 0x7F7F, 0xFF7F, 0x0001, 0x8001]
+    flat = buf.view(torch.int16)
+    gen = torch.Generator().manual_seed(12)
+    for j, i in enumerate(torch.randperm(flat.numel(), generator=gen)[:6 * len(specials)].tolist()):
+        flat[i] = np.int16(np.uint16(specials[j % len(specials)]))
+    with np.errstate(all="ignore"):  # NaN and infinity arithmetic is the point here
+        wq, wkc, wvc = N.norm_rope_append(u16(buf), row_stride, u16(qw), u16(kw), 1e-6, u16(kc), u16(vc),
+                                          pos.numpy(), slots.numpy(), table.numpy(), rows, hq, hkv, True, 4096, cs)
+    q_out = torch.empty(rows, hq, 128, dtype=buf.dtype, device=dev)
+    kcd, vcd = kc.to(dev), vc.to(dev)
+    feattn.norm_rope_append(buf.to(dev), row_stride, qw.to(dev), kw.to(dev), 1e-6, q_out, kcd, vcd, pos.to(dev),
+                            slots.to(dev), table.to(dev), rows, hq, hkv, True, 4096, cs)
+    torch.cuda.synchronize()
+    assert (wq == 0x7FC0).any()  # the NaN path is exercised
+    assert np.array_equal(u16(q_out), wq)
+    assert np.array_equal(u16(kcd).reshape(cs, -1), wkc)
+    assert np.array_equal(u16(vcd).reshape(cs, -1), wvc)
+
+
 @pytest.mark.parametrize("bf16", [True, False])
 def test_norm_rope_append_equals_unfused_sequence(dev, bf16):
     """Bit-identical to src/cuda_model.cpp:91-95 run as separate calls:

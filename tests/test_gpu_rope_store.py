@@ -59,6 +59,53 @@ def test_rope_bit_exact(dev, bf16, hq, hkv, rows):
     assert np.array_equal(u16(kd), want_k)
 
 
+def _plant_specials(t, seed):
+    """Writes bf16 special values at seeded positions of t: NaNs with
+    several payloads and signs (quiet and signalling), infinities, values
+    whose rotation overflows, subnormals and signed zeros."""
+    specials = [0x7FC0, 0x7FC1, 0x7F81, 0xFFC0, 0x7FFF, 0x7F80, 0xFF80, 0x7F7F, 0xFF7F, 0x0001, 0x8001,
+                0x007F, 0x0000, 0x8000]
+    flat = t.view(torch.int16).view(-1)
+    gen = torch.Generator().manual_seed(seed)
+    idx = torch.randperm(flat.numel(), generator=gen)[:8 * len(specials)]
+    for j, i in enumerate(idx.tolist()):
+        flat[i] = np.int16(np.uint16(specials[j % len(specials)]))
+    return t
+
+
+@pytest.mark.parametrize("hq,hkv,rows", [(32, 8, 61), (16, 8, 7)])
+def test_rope_special_values_bit_exact(dev, hq, hkv, rows):
+    """bf16 rounding of NaN (0x7fc0 whatever the payload), infinities,
+    overflow and subnormals matches the oracle bit for bit, in fe_rope and
+    in the fused append."""
+    gen = torch.Generator().manual_seed(rows)
+    q = _plant_specials((torch.randn(rows, hq, 128, generator=gen) * 4).to(torch.bfloat16), 1)
+    k = _plant_specials((torch.randn(rows, hkv, 128, generator=gen) * 4).to(torch.bfloat16), 2)
+    v = torch.randn(rows, hkv, 128, generator=gen).to(torch.bfloat16)
+    table = W.rope_table(8192, 1e6)
+    pos = torch.randint(0, 8192, (rows,), generator=gen)
+    with np.errstate(all="ignore"):  # inf * 0 and overflow are the point here
+        want_q, want_k = R.rope(u16(q), u16(k), pos.numpy(), table.numpy(), rows, hq, hkv, 128, True, 8192)
+    qd, kd = q.to(dev), k.to(dev)
+    feattn.rope(qd, kd, pos.to(dev), table.to(dev), rows, hq, hkv, 128, True, 8192)
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(qd), want_q)
+    assert np.array_equal(u16(kd), want_k)
+    slots = torch.randperm(4 * rows, generator=gen)[:rows].clone()
+    kc = torch.zeros(4 * rows, hkv, 128, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    with np.errstate(all="ignore"):
+        wq, wkc, wvc = R.rope_append(u16(q), u16(k), u16(v), u16(kc), u16(vc), pos.numpy(), slots.numpy(),
+                                     table.numpy(), rows, hq, hkv, 128, True, 8192, 4 * rows)
+    qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
+    feattn.rope_append(qd, k.to(dev), v.to(dev), kcd, vcd, pos.to(dev), slots.to(dev), table.to(dev), rows, hq,
+                       hkv, 128, True, 8192, 4 * rows)
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(qd), wq)
+    assert np.array_equal(u16(kcd).reshape(wkc.shape), wkc)
+    assert np.array_equal(u16(vcd).reshape(wvc.shape), wvc)
+
+
 def test_rope_rejects_alias(dev):
     q = torch.zeros(2, 2, 128, dtype=torch.bfloat16, device=dev)
     pos = torch.zeros(2, dtype=torch.int64, device=dev)
