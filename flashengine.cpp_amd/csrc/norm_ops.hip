@@ -120,8 +120,9 @@ __device__ __forceinline__ void normalize_head(u32x4& x, u32x4& y, u32x4 wl, u32
 // are copied to the V cache.  Row r of the input holds q | k | v heads at
 // qkv + r * row_stride.  Rows whose slot is outside [0, cache_slots) write
 // no cache entry; rows whose position is outside [0, max_pos) are normalized
-// but not rotated.
-template <bool BF16>
+// but not rotated.  I: index type of the flat work range (uint32_t when it
+// fits, which keeps the (row, head) split a 32-bit division).
+template <bool BF16, typename I>
 __global__ __launch_bounds__(256) void norm_rope_append_kernel(
     const uint16_t* __restrict__ qkv, int64_t row_stride, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
@@ -132,11 +133,10 @@ __global__ __launch_bounds__(256) void norm_rope_append_kernel(
   const int64_t total = (int64_t)rows * heads * 8;   // a multiple of 8: groups never straddle the end
   const int c = threadIdx.x & 7;
   const int ch = c < 4 ? c : 11 - c;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t unit = idx >> 3;
-    const int head = (int)(unit % heads);
-    const int64_t row = unit / heads;
+  for (I idx = (I)blockIdx.x * blockDim.x + threadIdx.x; idx < (I)total; idx += (I)gridDim.x * blockDim.x) {
+    const I unit = idx >> 3;
+    const int head = (int)(unit % (I)heads);
+    const int64_t row = (int64_t)(unit / (I)heads);
     int64_t slot = 0;
     if (head >= hq) {
       slot = slots[row];
@@ -228,14 +228,14 @@ hipError_t launch_norm_rope_append(const void* qkv, int64_t row_stride, const vo
   const int64_t work = (int64_t)rows * (hq + 2 * hkv) * 8;
   if (work == 0) return hipSuccess;
   const int grid = grid_for(work);
-  if (bf16)
-    hipLaunchKernelGGL(norm_rope_append_kernel<true>, dim3(grid), dim3(256), 0, st, (const uint16_t*)qkv, row_stride,
-                       (const uint16_t*)qw, (const uint16_t*)kw, eps, (uint16_t*)q_out, (uint16_t*)kc, (uint16_t*)vc,
-                       pos, slots, cache, rows, hq, hkv, max_pos, cache_slots);
-  else
-    hipLaunchKernelGGL(norm_rope_append_kernel<false>, dim3(grid), dim3(256), 0, st, (const uint16_t*)qkv,
-                       row_stride, (const uint16_t*)qw, (const uint16_t*)kw, eps, (uint16_t*)q_out, (uint16_t*)kc,
-                       (uint16_t*)vc, pos, slots, cache, rows, hq, hkv, max_pos, cache_slots);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, (const uint16_t*)qkv, row_stride, (const uint16_t*)qw,
+                       (const uint16_t*)kw, eps, (uint16_t*)q_out, (uint16_t*)kc, (uint16_t*)vc, pos, slots, cache,
+                       rows, hq, hkv, max_pos, cache_slots);
+  };
+  const bool narrow = work <= INT32_MAX;  // idx + grid stride stays below 2^32
+  if (bf16) narrow ? go(norm_rope_append_kernel<true, uint32_t>) : go(norm_rope_append_kernel<true, int64_t>);
+  else narrow ? go(norm_rope_append_kernel<false, uint32_t>) : go(norm_rope_append_kernel<false, int64_t>);
   return hipGetLastError();
 }
 

@@ -80,8 +80,9 @@ __global__ __launch_bounds__(256) void store_kernel_scalar(const uint16_t* __res
 
 // Fused rope + append.  Work unit = (row, head in [0, hq + hkv), chunk):
 // query heads rotate q in place; kv heads rotate k into the K cache at the
-// row's slot and copy both halves of v into the V cache.
-template <bool BF16>
+// row's slot and copy both halves of v into the V cache.  I: index type of
+// the flat work range (uint32_t when it fits: 32-bit divisions).
+template <bool BF16, typename I>
 __global__ __launch_bounds__(256) void rope_append_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                           const uint16_t* __restrict__ v, uint16_t* __restrict__ kc,
                                                           uint16_t* __restrict__ vc, const int64_t* __restrict__ pos,
@@ -91,12 +92,11 @@ __global__ __launch_bounds__(256) void rope_append_kernel(uint16_t* __restrict__
   const int cpr = dim >> 4;
   const int half = dim >> 1;
   const int64_t total = (int64_t)rows * (hq + hkv) * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(idx % cpr);
-    const int64_t rh = idx / cpr;
-    const int head = (int)(rh % (hq + hkv));
-    const int64_t row = rh / (hq + hkv);
+  for (I idx = (I)blockIdx.x * blockDim.x + threadIdx.x; idx < (I)total; idx += (I)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % (I)cpr);
+    const I rh = idx / (I)cpr;
+    const int head = (int)(rh % (I)(hq + hkv));
+    const int64_t row = (int64_t)(rh / (I)(hq + hkv));
     const int64_t p = pos[row];
     const bool rot = p >= 0 && p < max_pos;
     const float* cs = cache + (rot ? p : 0) * dim + 8 * c;
@@ -169,14 +169,13 @@ hipError_t launch_rope_append(void* q, const void* k, const void* v, void* kc, v
   const int64_t work = (int64_t)rows * (hq + hkv) * (dim >> 4);
   if (work == 0) return hipSuccess;
   const int grid = grid_for(work);
-  if (bf16)
-    hipLaunchKernelGGL(rope_append_kernel<true>, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (const uint16_t*)k,
-                       (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, pos, slots, cache, rows, hq, hkv, dim,
-                       max_pos, cache_slots);
-  else
-    hipLaunchKernelGGL(rope_append_kernel<false>, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (const uint16_t*)k,
-                       (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, pos, slots, cache, rows, hq, hkv, dim,
-                       max_pos, cache_slots);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (uint16_t*)kc, (uint16_t*)vc, pos, slots, cache, rows, hq, hkv, dim, max_pos, cache_slots);
+  };
+  const bool narrow = work <= INT32_MAX;  // idx + grid stride stays below 2^32
+  if (bf16) narrow ? go(rope_append_kernel<true, uint32_t>) : go(rope_append_kernel<true, int64_t>);
+  else narrow ? go(rope_append_kernel<false, uint32_t>) : go(rope_append_kernel<false, int64_t>);
   return hipGetLastError();
 }
 
