@@ -169,6 +169,11 @@ def _prefill(b, dev, res):
     ra = lambda i: feattn.rope_append(q, k, v, kc, vc, pos, slots, table, b.rows, b.hq, b.hkv, 128,
                                       True, 8192, b.cache_slots)
     ms_ra = event_time_ms(ra, 20, 3)
+    # the reference's two calls (src/cuda_model.cpp:94-95), each on its own
+    ro = lambda i: feattn.rope(q, k, pos, table, b.rows, b.hq, b.hkv, 128, True, 8192)
+    ms_ro = event_time_ms(ro, 20, 3)
+    st = lambda i: feattn.store(k, v, kc, vc, slots, b.rows, b.hkv * 128, True, b.cache_slots)
+    ms_st = event_time_ms(st, 20, 3)
     # the same new tokens through the fused q/k RMSNorm + RoPE + append of a
     # [rows][q | k | v] projection (src/cuda_model.cpp:91-95 in one pass)
     qkv = torch.randn(b.rows, (b.hq + 2 * b.hkv) * 128, device=dev).to(torch.bfloat16)
@@ -184,6 +189,8 @@ def _prefill(b, dev, res):
         "gflop": round(flops / 1e9, 2),
         "rope_append_ms": round(ms_ra, 4),
         "rope_append_gbs": round(W.rope_append_bytes(b) / ms_ra / 1e6, 1),
+        "rope_ms": round(ms_ro, 4), "rope_gbs": round(W.rope_bytes(b) / ms_ro / 1e6, 1),
+        "store_ms": round(ms_st, 4), "store_gbs": round(W.store_bytes(b) / ms_st / 1e6, 1),
         "norm_rope_append_ms": round(ms_nra, 4),
         "norm_rope_append_gbs": round(W.norm_rope_append_bytes(b) / ms_nra / 1e6, 1)}
     log("prefill", res["prefill_qwen3_8b"])

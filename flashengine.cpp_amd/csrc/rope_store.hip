@@ -14,20 +14,20 @@
 
 namespace feattn {
 
-// In-place rope on q [rows][hq][dim] and k [rows][hkv][dim].
-template <bool BF16>
+// In-place rope on q [rows][hq][dim] and k [rows][hkv][dim].  I: index type
+// of the flat work range (uint32_t when it fits: 32-bit divisions).
+template <bool BF16, typename I>
 __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
                                                    const int64_t* __restrict__ pos,
                                                    const float* __restrict__ cache, int rows, int hq, int hkv,
                                                    int dim, int max_pos) {
   const int cpr = dim >> 4;  // 8-pair chunks per head
   const int64_t total = (int64_t)rows * (hq + hkv) * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(idx % cpr);
-    const int64_t rh = idx / cpr;
-    const int head = (int)(rh % (hq + hkv));
-    const int64_t row = rh / (hq + hkv);
+  for (I idx = (I)blockIdx.x * blockDim.x + threadIdx.x; idx < (I)total; idx += (I)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % (I)cpr);
+    const I rh = idx / (I)cpr;
+    const int head = (int)(rh % (I)(hq + hkv));
+    const int64_t row = (int64_t)(rh / (I)(hq + hkv));
     const int64_t p = pos[row];
     if (p < 0 || p >= max_pos) continue;
     uint16_t* base = head < hq ? q + (row * hq + head) * dim : k + (row * hkv + (head - hq)) * dim;
@@ -42,17 +42,18 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ q, uin
 }
 
 // kc[slot][:] = k[row][:], vc[slot][:] = v[row][:]; padding rows (slot < 0)
-// and out-of-range slots are skipped.  `chunks` = width / 8.
+// and out-of-range slots are skipped.  `chunks` = width / 8.  I: index type
+// of the flat work range (uint32_t when it fits).
+template <typename I>
 __global__ __launch_bounds__(256) void store_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                     const int64_t* __restrict__ slots, int rows, int chunks,
                                                     int64_t cache_slots) {
   const int64_t total = (int64_t)rows * chunks;
   const int64_t width = (int64_t)chunks * 8;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = idx / chunks;
-    const int64_t c = idx - row * chunks;
+  for (I idx = (I)blockIdx.x * blockDim.x + threadIdx.x; idx < (I)total; idx += (I)gridDim.x * blockDim.x) {
+    const int64_t row = (int64_t)(idx / (I)chunks);
+    const int64_t c = (int64_t)idx - row * chunks;
     const int64_t slot = slots[row];
     if (slot < 0 || slot >= cache_slots) continue;
     stv(kc + slot * width + 8 * c, ldv(k + row * width + 8 * c));
@@ -139,12 +140,13 @@ hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache,
   const int64_t work = (int64_t)rows * (hq + hkv) * (dim >> 4);
   if (work == 0) return hipSuccess;
   const int grid = grid_for(work);
-  if (bf16)
-    hipLaunchKernelGGL(rope_kernel<true>, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (uint16_t*)k, pos, cache, rows,
-                       hq, hkv, dim, max_pos);
-  else
-    hipLaunchKernelGGL(rope_kernel<false>, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (uint16_t*)k, pos, cache,
-                       rows, hq, hkv, dim, max_pos);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, (uint16_t*)q, (uint16_t*)k, pos, cache, rows, hq, hkv,
+                       dim, max_pos);
+  };
+  const bool narrow = work <= INT32_MAX;  // idx + grid stride stays below 2^32
+  if (bf16) narrow ? go(rope_kernel<true, uint32_t>) : go(rope_kernel<true, int64_t>);
+  else narrow ? go(rope_kernel<false, uint32_t>) : go(rope_kernel<false, int64_t>);
   return hipGetLastError();
 }
 
@@ -153,8 +155,13 @@ hipError_t launch_store(const void* k, const void* v, void* kc, void* vc, const 
   if (rows == 0 || width == 0) return hipSuccess;
   if (width % 8 == 0) {
     const int chunks = width / 8;
-    hipLaunchKernelGGL(store_kernel, dim3(grid_for((int64_t)rows * chunks)), dim3(256), 0, st, (const uint16_t*)k,
-                       (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, slots, rows, chunks, cache_slots);
+    const int64_t work = (int64_t)rows * chunks;
+    if (work <= INT32_MAX)  // idx + grid stride stays below 2^32
+      hipLaunchKernelGGL(store_kernel<uint32_t>, dim3(grid_for(work)), dim3(256), 0, st, (const uint16_t*)k,
+                         (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, slots, rows, chunks, cache_slots);
+    else
+      hipLaunchKernelGGL(store_kernel<int64_t>, dim3(grid_for(work)), dim3(256), 0, st, (const uint16_t*)k,
+                         (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, slots, rows, chunks, cache_slots);
   } else {
     hipLaunchKernelGGL(store_kernel_scalar, dim3(grid_for((int64_t)rows * width)), dim3(256), 0, st,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)kc, (uint16_t*)vc, slots, rows, width,

@@ -250,6 +250,18 @@ def norm_rope_append_bytes(b: Batch, elem: int = 2) -> int:
     return b.rows * per_row
 
 
+def rope_bytes(b: Batch, elem: int = 2) -> int:
+    """In-place RoPE of the new tokens (fe_rope): q and k read and written,
+    the pos read, the cos|sin row read: per new token."""
+    return b.rows * (2 * (b.hq + b.hkv) * HEAD_DIM * elem + 8 + HEAD_DIM * 4)
+
+
+def store_bytes(b: Batch, elem: int = 2) -> int:
+    """Paged store of the new tokens (fe_store): k and v read, k and v cache
+    writes, the slot read: per new token."""
+    return b.rows * (4 * b.hkv * HEAD_DIM * elem + 8)
+
+
 def rope_append_bytes(b: Batch, elem: int = 2) -> int:
     """q read+write, k and v read, k and v cache writes, pos and slot reads,
     the cos|sin row read: per new token."""
