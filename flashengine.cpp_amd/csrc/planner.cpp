@@ -39,20 +39,26 @@ void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>
   std::stable_sort(items.begin(), items.end(),
                    [](const WorkItem& x, const WorkItem& y) { return x.cost > y.cost; });
   const int n = std::max(1, std::min<int>(slots, (int)items.size()));
-  std::vector<int64_t> load(n, 0);
   std::vector<int> share(items.size());
-  // (load, share) min-heap
-  std::vector<std::pair<int64_t, int>> heap;
-  heap.reserve(n);
-  for (int k = 0; k < n; ++k) heap.emplace_back(0, k);
-  auto cmp = [](const std::pair<int64_t, int>& x, const std::pair<int64_t, int>& y) { return x > y; };
-  std::make_heap(heap.begin(), heap.end(), cmp);
+  // Binary min-heap of (load << 20 | share) keys: the root is the least-loaded
+  // share, the lowest index among equals.  Each item raises the root's load
+  // and sifts it down (one pass instead of a pop and a push).
+  constexpr int kShareBits = 20;  // shares (tile workgroups) < 2^20; loads < 2^43
+  std::vector<uint64_t> heap(n);
+  for (int k = 0; k < n; ++k) heap[k] = (uint64_t)k;  // ascending: already a heap
   for (size_t i = 0; i < items.size(); ++i) {
-    std::pop_heap(heap.begin(), heap.end(), cmp);
-    auto& top = heap.back();
-    share[i] = top.second;
-    top.first += items[i].cost;
-    std::push_heap(heap.begin(), heap.end(), cmp);
+    share[i] = (int)(heap[0] & ((uint64_t(1) << kShareBits) - 1));
+    const uint64_t key = heap[0] + ((uint64_t)items[i].cost << kShareBits);
+    size_t h = 0;
+    for (;;) {
+      size_t c = 2 * h + 1;
+      if (c >= (size_t)n) break;
+      if (c + 1 < (size_t)n && heap[c + 1] < heap[c]) ++c;
+      if (heap[c] >= key) break;
+      heap[h] = heap[c];
+      h = c;
+    }
+    heap[h] = key;
   }
   off.assign(n + 1, 0);
   for (size_t i = 0; i < items.size(); ++i) ++off[share[i] + 1];
