@@ -289,6 +289,7 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
     int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 8 + pairs - 1) / pairs);
     for (;;) {
       ml.tile.clear();
+      ml.tile.reserve((size_t)std::min<int64_t>(pairs * want, sh.item_cap + 1));  // at most want pieces per pair
       ml.merge.clear();
       ml.partial_rows = out.decode_partials;
       for (int b = 0; b < batch; ++b) {
