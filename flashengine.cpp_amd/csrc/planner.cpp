@@ -36,8 +36,24 @@ std::vector<int64_t> cut_uniform(int64_t stream, int64_t quota) {
 // least-loaded share -- and regroups them share by share (longest first
 // inside a share).  off receives the CSR offsets of the shares in use.
 void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off) {
-  std::stable_sort(items.begin(), items.end(),
-                   [](const WorkItem& x, const WorkItem& y) { return x.cost > y.cost; });
+  // Stable sort by decreasing cost: a counting sort over the (small,
+  // non-negative) costs, else the comparison sort.
+  int32_t cmin = 0, cmax = 0;
+  for (const WorkItem& w : items) {
+    cmin = std::min(cmin, w.cost);
+    cmax = std::max(cmax, w.cost);
+  }
+  if (cmin >= 0 && cmax <= (1 << 16)) {
+    std::vector<int32_t> start((size_t)cmax + 2, 0);
+    for (const WorkItem& w : items) ++start[(size_t)(cmax - w.cost) + 1];
+    for (size_t c = 1; c < start.size(); ++c) start[c] += start[c - 1];
+    std::vector<WorkItem> sorted(items.size());
+    for (const WorkItem& w : items) sorted[start[(size_t)(cmax - w.cost)]++] = w;
+    items.swap(sorted);
+  } else {
+    std::stable_sort(items.begin(), items.end(),
+                     [](const WorkItem& x, const WorkItem& y) { return x.cost > y.cost; });
+  }
   const int n = std::max(1, std::min<int>(slots, (int)items.size()));
   std::vector<int> share(items.size());
   // Binary min-heap of (load << 20 | share) keys: the root is the least-loaded
