@@ -28,3 +28,28 @@ def dev():
     feattn.lib()  # raises if libfeattn.so is not built: no silent fallback
     torch.cuda.set_device(0)
     return torch.device("cuda", 0)
+
+
+# (name, max |out err|, max |out err| / (atol + rtol |want|), max |lse err|)
+# of the full-size sampled parity checks, printed in the session summary.
+_ERRORS = []
+
+
+@pytest.fixture
+def err_report():
+    def record(name, out, lse, want_out, want_lse, atol=1e-2, rtol=1e-2):
+        d = (out.float() - want_out.float()).abs()
+        ratio = (d / (atol + rtol * want_out.float().abs())).max().item()
+        _ERRORS.append((name, d.max().item(), ratio, (lse - want_lse).abs().max().item()))
+
+    return record
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not _ERRORS:
+        return
+    terminalreporter.write_sep("-", "attention parity headroom (full-size sampled rows)")
+    for name, e, ratio, le in _ERRORS:
+        terminalreporter.write_line(
+            f"{name:14s} max|out err| {e:.3e}  (fraction of the 1e-2+1e-2|b| bound: {ratio:.3f})  "
+            f"max|lse err| {le:.3e}")

@@ -1,0 +1,129 @@
+"""Exact visible-token counts on every benchmarked shape, through the C ABI.
+
+With q = k = 0 every visible key gets the same weight, so (definitions of
+src/portable_gpu_ops.cpp:30-31; known-answer pattern of
+tests/ascend_ops_tests.cpp:21,44):
+  * LSE = ln(n) exactly up to the last fp32 rounding, n = visible keys of the
+    row (end-aligned causal: len - qlen + i + 1; non-causal: len).  One key
+    dropped or added moves LSE by ~1/n, 3e-5 at n = 32768: the 1e-5 bound
+    pins n exactly on every split boundary and last partial block.
+  * out = mean of the visible V rows.  V of token t, kv head g is the one-hot
+    vector e_{(t + 7g) mod 128}, so out[d] = (#visible t with t = d - 7g
+    mod 128) / n: the residue counts show which tokens were read, not only
+    how many.  Slots past a sequence's end and the dummy page hold ones in
+    every dim, so a stale read moves every element.
+fp16 runs compare out at 2e-3 relative (a missing key moves one element by
+128/n >= 3.9e-3 at n = 32768); bf16 runs at the attention tolerance 1e-2.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import feattn
+from feattn import workloads as W
+
+pytestmark = pytest.mark.gpu
+LSE_EXACT = 1e-5
+
+
+def visible_counts(b, causal):
+    """n per query row (int64 [rows])."""
+    n = np.zeros(b.rows, dtype=np.int64)
+    for s in range(b.batch):
+        L, ln = b.qlens[s], b.lens[s]
+        i = np.arange(L)
+        n[b.qo[s]:b.qo[s + 1]] = (ln - L + i + 1) if causal else ln
+    return n
+
+
+def residue_v_cache(b, dtype):
+    """V cache: token t of every sequence, kv head g -> one-hot at (t + 7g) % 128;
+    every other slot (stale tail of the last page, unused and dummy pages) all ones."""
+    vc = np.ones((b.cache_slots, b.hkv, 128), dtype=np.float16)  # 0 and 1 are exact in both 16-bit types
+    g = np.arange(b.hkv)
+    for s in range(b.batch):
+        ln = b.lens[s]
+        t = np.arange(ln)
+        table = np.asarray(b.tables[s], dtype=np.int64)
+        slot = table[t // b.page] * b.page + t % b.page
+        vc[slot] = 0.0
+        d = (t[:, None] + 7 * g[None, :]) % 128
+        vc[slot[:, None], g[None, :], d] = 1.0
+    return torch.from_numpy(vc.reshape(b.blocks + 1, b.page, b.hkv, 128)).to(dtype)
+
+
+def expected_out(b, n, rows):
+    """out[r, h, d] for the chosen rows (float64 [len(rows), hq, 128])."""
+    G = b.group
+    h = np.arange(b.hq)
+    d = np.arange(128)
+    r = (d[None, :] - 7 * (h[:, None] // G)) % 128          # [hq, 128] first token of the class
+    nn = n[rows][:, None, None]
+    cnt = np.where(r[None] < nn, (nn - 1 - r[None]) // 128 + 1, 0)
+    return cnt / nn
+
+
+def run_case(dev, b, causal, dtype, plan_pages=None):
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    q = torch.zeros(b.rows, b.hq, 128, dtype=dt, device=dev)
+    kc = torch.zeros(b.blocks + 1, b.page, b.hkv, 128, dtype=dt, device=dev)
+    vc = residue_v_cache(b, dt).to(dev)
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, plan_pages or b.max_pages(), dt == torch.bfloat16,
+                       b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    out = torch.full_like(q, float("nan"))
+    lse = torch.full((b.rows, b.hq), float("nan"), device=dev)
+    plan.run(q, kc, vc, out, causal=causal, lse=lse)
+    torch.cuda.synchronize()
+    plan.close()
+    n = visible_counts(b, causal)
+    want_lse = torch.from_numpy(np.log(n.astype(np.float64))).float()[:, None].expand(b.rows, b.hq)
+    lse = lse.cpu()
+    err_lse = (lse - want_lse).abs().max().item()
+    assert err_lse <= LSE_EXACT, f"LSE off by {err_lse:.3g} (count pin 1e-5)"
+    # out: every row for small batches, a strided sample of up to 2048 rows otherwise
+    rows = np.arange(b.rows) if b.rows <= 2048 else np.unique(np.linspace(0, b.rows - 1, 2048).astype(np.int64))
+    got = out.cpu()[torch.from_numpy(rows)].double().numpy()
+    want = expected_out(b, n, rows)
+    rtol = 2e-3 if dtype == "f16" else 1e-2
+    bad = np.abs(got - want) > rtol * want + 1e-6
+    assert not bad.any(), f"{int(bad.sum())} out elements off, first at {np.argwhere(bad)[0].tolist()}"
+    return err_lse
+
+
+SHAPES = {
+    "decode8b": (lambda: W.qwen3_8b_decode(), True),
+    "long16x32k": (lambda: W.long_decode(), True),
+    "prefill8b": (lambda: W.qwen3_8b_prefill(), True),
+    "dflash": (lambda: W.dflash_block(), False),
+    "mixed30b": (lambda: W.qwen3_30b_mixed(), True),
+}
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_exact_counts_full_shapes(dev, name, dtype):
+    make, causal = SHAPES[name]
+    b = make()
+    run_case(dev, b, causal, dtype)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_exact_counts_prefill_chunks_non_causal_and_causal(dev, causal):
+    """Chunks and verify rows with both masks: every chunk boundary against
+    the 64-token tile and 16-token page grids."""
+    b = W.make_batch(32, 8, starts=[0, 15, 16, 17, 63, 64, 65, 1000, 2047],
+                     qlens=[1, 2, 3, 64, 65, 127, 129, 300, 33], seed=77, extra_pages=2)
+    run_case(dev, b, causal, "f16")
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 2), (24, 6), (40, 8), (8, 8)])
+def test_exact_counts_head_layouts(dev, hq, hkv):
+    """Head layouts whose decode workgroups hold 2 or 1 wavefronts (hkv = 2,
+    6) and non-power-of-two groups, decode and chunk rows mixed."""
+    b = W.make_batch(hq, hkv, starts=[4095, 0, 777, 5000, 31], qlens=[1, 1, 1, 2, 90], seed=hq + hkv,
+                     extra_pages=1)
+    run_case(dev, b, True, "f16")

@@ -199,3 +199,37 @@ def test_rope_store_match_reference_aten_on_device(dev, bf16):
     ref_lib.store(k1, v, kc2, vc2, slots, b.rows, 1024, bf16, b.cache_slots)
     torch.cuda.synchronize()
     assert torch.equal(kc1[:-1], kc2[:-1]) and torch.equal(vc1[:-1], vc2[:-1])
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_rope_append_full_prefill_step(dev, bf16):
+    """The benchmarked chunked-prefill step: all 8192 new tokens of the
+    8-sequence Qwen3-8B batch appended with RoPE (theta 1e6) in one call,
+    bit-identical to fe_rope then fe_store on the device and to the oracle,
+    with every slot outside the new tokens left untouched."""
+    b = W.qwen3_8b_prefill()
+    dt = dtype_of(bf16)
+    gen = torch.Generator().manual_seed(9)
+    q = torch.randn(b.rows, 32, 128, generator=gen).to(dt)
+    k = torch.randn(b.rows, 8, 128, generator=gen).to(dt)
+    v = torch.randn(b.rows, 8, 128, generator=gen).to(dt)
+    kc = torch.randn(b.blocks + 1, 16, 8, 128, generator=gen).to(dt)
+    vc = torch.randn(b.blocks + 1, 16, 8, 128, generator=gen).to(dt)
+    pos, slots = torch.from_numpy(b.positions), torch.from_numpy(b.slots)
+    table = W.rope_table(4096, 1e6)
+    args = lambda *t: [x.to(dev) for x in t]
+    qd, kd, vd, kcd, vcd, posd, slotsd, tabd = args(q, k, v, kc, vc, pos, slots, table)
+    feattn.rope_append(qd, kd, vd, kcd, vcd, posd, slotsd, tabd, b.rows, 32, 8, 128, bf16, 4096, b.cache_slots)
+    q2, k2, kc2, vc2 = qd.new_tensor(q), kd.new_tensor(k), kcd.new_tensor(kc), vcd.new_tensor(vc)
+    feattn.rope(q2, k2, posd, tabd, b.rows, 32, 8, 128, bf16, 4096)
+    feattn.store(k2, vd, kc2, vc2, slotsd, b.rows, 8 * 128, bf16, b.cache_slots)
+    torch.cuda.synchronize()
+    assert torch.equal(qd, q2) and torch.equal(kcd, kc2) and torch.equal(vcd, vc2)
+    wq, wkc, wvc = R.rope_append(u16(q), u16(k), u16(v), u16(kc), u16(vc), b.positions, b.slots,
+                                 table.numpy(), b.rows, 32, 8, 128, bf16, 4096, b.cache_slots)
+    assert np.array_equal(u16(qd), wq)
+    assert np.array_equal(u16(kcd).reshape(b.cache_slots, -1), wkc)
+    assert np.array_equal(u16(vcd).reshape(b.cache_slots, -1), wvc)
+    untouched = np.ones(b.cache_slots, dtype=bool)
+    untouched[b.slots] = False
+    assert np.array_equal(u16(kcd).reshape(b.cache_slots, -1)[untouched], u16(kc).reshape(b.cache_slots, -1)[untouched])
