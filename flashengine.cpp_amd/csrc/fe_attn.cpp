@@ -26,7 +26,6 @@ namespace feattn {
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st);
 int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
-hipError_t launch_wide(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
                        bool bf16, int max_pos, hipStream_t st);
@@ -69,7 +68,7 @@ int share_cap(const PlanShape& sh) { return std::max(1, sh.decode_waves / sh.hkv
 
 // Offsets of the regions inside the metadata arena (same layout on host and device).
 struct Layout {
-  size_t seqs, pages, counts, zero, dshare, decode, tile[2], tshare[2], wide[2], wshare[2], merge[2], total;
+  size_t seqs, pages, counts, dshare, decode, tile[2], tshare[2], merge[2], total;
 };
 
 Layout make_layout(const PlanShape& sh) {
@@ -81,8 +80,6 @@ Layout make_layout(const PlanShape& sh) {
   off = align256(off + sizeof(int32_t) * (size_t)sh.max_batch * sh.max_pages);
   l.counts = off;
   off = align256(off + sizeof(int32_t) * 8);
-  l.zero = off;  // 256 zero bytes, never written after create
-  off = align256(off + 256);
   l.dshare = off;
   off = align256(off + sizeof(ShareStart) * (size_t)share_cap(sh));
   l.decode = off;
@@ -92,10 +89,6 @@ Layout make_layout(const PlanShape& sh) {
     off = align256(off + sizeof(WorkItem) * sh.item_cap);
     l.tshare[m] = off;
     off = align256(off + sizeof(int32_t) * ((size_t)sh.tile_slots + 1));
-    l.wide[m] = off;
-    off = align256(off + sizeof(WorkItem) * sh.item_cap);
-    l.wshare[m] = off;
-    off = align256(off + sizeof(int32_t) * ((size_t)sh.wide_slots + 1));
   }
   for (int m = 0; m < 2; ++m) {
     l.merge[m] = off;
@@ -106,7 +99,7 @@ Layout make_layout(const PlanShape& sh) {
 }
 
 // counts[] indices
-enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4, kCntWide0 = 5, kCntWide1 = 6 };
+enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
 
 // Split-KV slot budget: as many (row, all heads) partial slots as 64 MiB of
 // fp32 rows would hold; the rows are stored in 16 bits, so they take half.
@@ -135,13 +128,12 @@ struct fe_attn_plan {
   bool prepared = false;
   bool graph = false;
   int graph_nc = 0;
-  int graph_tile = -1;  // the first graph prepare's kernels: bit 0 tile work, bit 1 wide work
-  int n_decode = 0, n_tile[2] = {0, 0}, n_wide[2] = {0, 0}, n_merge[2] = {0, 0};
+  int graph_tile = -1;  // the first graph prepare had tile work (1) or not (0)
+  int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
-  int n_wshare[2] = {0, 0};  // wide shares (workgroups) in use per mask mode
   int decode_wg = 8;  // wavefronts per decode workgroup
   int decode_nc = 16;
-  int grid_decode_cap = 0, grid_tile_cap = 0, grid_wide_cap = 0, grid_merge_cap = 0;
+  int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
 };
 
 extern "C" {
@@ -177,7 +169,6 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
 
   sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
   sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
-  sh.wide_slots = sh.num_cus;      // 1 resident 512-thread wide workgroup per CU
   auto* p = new (std::nothrow) fe_attn_plan();
   if (p == nullptr) return fail(FE_ENOMEM, "out of host memory");
   p->sh = sh;
@@ -187,7 +178,6 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   p->decode_wg = decode_wg_waves(hkv);
   p->grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / p->decode_wg;  // persistent: every workgroup resident
   p->grid_tile_cap = sh.tile_slots;
-  p->grid_wide_cap = sh.wide_slots;
   p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head pair) units per workgroup
   auto cleanup = [&](int code, const std::string& msg) {
     fe_attn_plan_destroy(p);
@@ -241,13 +231,12 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     if (nc > graph_nc)
       return fail(FE_EINVAL, "graph plan layout changed: decode rows per sequence grew after capture");
     nc = graph_nc;
-    // Likewise which of the tile and wide kernels are launched at all: a
-    // graph of decode-only steps carries no tile launch, and a later prepare
-    // may not bring tile work to it.
-    const int tile = (bp.mode[0].tile.empty() && bp.mode[1].tile.empty() ? 0 : 1) |
-                     (bp.mode[0].wide.empty() && bp.mode[1].wide.empty() ? 0 : 2);
+    // Likewise whether the tile kernel is launched at all: a graph of
+    // decode-only steps carries no tile launch, and a later prepare may not
+    // bring tile work to it.
+    const int tile = bp.mode[0].tile.empty() && bp.mode[1].tile.empty() ? 0 : 1;
     if (graph_tile < 0) graph_tile = tile;
-    if ((tile & ~graph_tile) != 0)
+    if (tile > graph_tile)
       return fail(FE_EINVAL, "graph plan layout changed: multi-row tile work after a capture without it");
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -275,8 +264,6 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   cnt[kCntTile1] = (int32_t)bp.mode[1].tile.size();
   cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
   cnt[kCntMerge1] = (int32_t)bp.mode[1].merge.size();
-  cnt[kCntWide0] = (int32_t)bp.mode[0].wide.size();
-  cnt[kCntWide1] = (int32_t)bp.mode[1].wide.size();
   std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
   const int tslots = p->sh.tile_slots;
   for (int m = 0; m < 2; ++m) {
@@ -289,13 +276,6 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     if (used > tslots) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: tile shares");
     int32_t* dst = reinterpret_cast<int32_t*>(h + l.tshare[m]);
     for (int k = 0; k <= tslots; ++k) dst[k] = k <= used && !off.empty() ? off[k] : (int32_t)bp.mode[m].tile.size();
-    std::memcpy(h + l.wide[m], bp.mode[m].wide.data(), sizeof(WorkItem) * bp.mode[m].wide.size());
-    const std::vector<int32_t>& woff = bp.mode[m].wide_off;
-    const int wused = woff.empty() ? 0 : (int)woff.size() - 1;
-    if (wused > p->sh.wide_slots) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: wide shares");
-    int32_t* wdst = reinterpret_cast<int32_t*>(h + l.wshare[m]);
-    for (int k = 0; k <= p->sh.wide_slots; ++k)
-      wdst[k] = k <= wused && !woff.empty() ? woff[k] : (int32_t)bp.mode[m].wide.size();
   }
   auto copy = [&](size_t off, size_t bytes) -> hipError_t {
     if (bytes == 0) return hipSuccess;
@@ -311,8 +291,6 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
     if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * ((size_t)tslots + 1));
     if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
-    if (e == hipSuccess) e = copy(l.wide[m], sizeof(WorkItem) * bp.mode[m].wide.size());
-    if (e == hipSuccess) e = copy(l.wshare[m], sizeof(int32_t) * ((size_t)p->sh.wide_slots + 1));
   }
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
   e = hipEventRecord(p->staged, st);
@@ -329,8 +307,6 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   for (int m = 0; m < 2; ++m) {
     p->n_tile[m] = (int)bp.mode[m].tile.size();
     p->n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
-    p->n_wide[m] = (int)bp.mode[m].wide.size();
-    p->n_wshare[m] = bp.mode[m].wide_off.empty() ? 0 : (int)bp.mode[m].wide_off.size() - 1;
     p->n_merge[m] = (int)bp.mode[m].merge.size();
   }
   return FE_OK;
@@ -381,17 +357,7 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
     e = launch_decode(d, p->bf16, p->decode_wg, p->decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
-  if (p->graph ? (p->graph_tile & 2) != 0 : p->n_wide[mode] > 0) {
-    AttnArgs t = a;
-    t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.wide[mode]);
-    t.n_items = counts + (mode ? kCntWide1 : kCntWide0);
-    t.tile_off = reinterpret_cast<const int32_t*>(p->dev + p->lay.wshare[mode]);
-    t.zero_row = reinterpret_cast<const uint16_t*>(p->dev + p->lay.zero);
-    const int grid = p->graph ? p->grid_wide_cap : p->n_wshare[mode];
-    e = launch_wide(t, p->bf16, causal != 0, std::max(grid, 1), st);
-    if (e != hipSuccess) return hip_fail(e, "wide kernel launch");
-  }
-  if (p->graph ? (p->graph_tile & 1) != 0 : p->n_tile[mode] > 0) {
+  if (p->graph ? p->graph_tile > 0 : p->n_tile[mode] > 0) {
     AttnArgs t = a;
     t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.tile[mode]);
     t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
@@ -533,7 +499,7 @@ int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int
   if (rc != FE_OK) return fail(rc, err);
   if (counts_out) {
     counts_out[0] = (int32_t)bp.decode.size() * hkv;
-    counts_out[1] = (int32_t)(bp.mode[1].tile.size() + bp.mode[1].wide.size());
+    counts_out[1] = (int32_t)bp.mode[1].tile.size();
     counts_out[2] = (int32_t)bp.mode[1].merge.size();
     counts_out[3] = bp.mode[1].partial_rows;
   }
@@ -579,7 +545,6 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch, int max
         emit(0, w);
       }
   for (const WorkItem& w : bp.mode[causal ? 1 : 0].tile) emit(1, w);
-  for (const WorkItem& w : bp.mode[causal ? 1 : 0].wide) emit(2, w);
   if (n_out) *n_out = n;
   return FE_OK;
 }

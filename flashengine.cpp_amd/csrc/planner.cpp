@@ -288,38 +288,29 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
     }
   }
 
-  // ---- tile and wide items, per mask mode.  Sequences of <= 128 (row,
-  // head) columns (verify rows, DFlash blocks) go to the tile kernel in items
-  // of <= 128 columns; wider ones (chunked prefill) to the wide kernel in
-  // items of <= 256 columns.  Long items are split into token ranges
-  // (multiples of the 64-token tile) when there are too few items for the
-  // device; splits are merged by log-sum-exp like decode pieces.
-  const int qr_tile = kTileCols / G;  // query rows per tile item
-  const int qr_wide = std::max(1, kWideCols / G);
+  // ---- tile items, per mask mode.
+  const int qr = kTileCols / G;  // query rows per tile item
   for (int causal = 0; causal < 2; ++causal) {
     ModeLists& ml = out.mode[causal];
     ml.partial_rows = out.decode_partials;
-    // (q block, kv head) pairs before splitting, to size the split factors.
-    int64_t tpairs = 0, wpairs = 0;
+    // (q tile, kv head) pairs before splitting, to size the split factor.
+    int64_t pairs = 0;
     for (int b = 0; b < batch; ++b) {
       const SeqInfo& s = out.seqs[b];
-      if (s.qlen * G > kTileCols) wpairs += (int64_t)ceil_div(s.qlen, qr_wide) * sh.hkv;
-      else if (s.qlen * G > kDecodeCols) tpairs += (int64_t)ceil_div(s.qlen, qr_tile) * sh.hkv;
+      if (s.qlen * G > kDecodeCols) pairs += (int64_t)ceil_div(s.qlen, qr) * sh.hkv;
     }
-    if (tpairs + wpairs == 0) continue;
-    // Aim for about 8 tile items per compute unit (2 resident workgroups,
-    // several rounds in longest-first order) and 4 wide items (1 resident
-    // workgroup); never split below 256 tokens.
-    int want_t = tpairs ? (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 8 + tpairs - 1) / tpairs) : 1;
-    int want_w = wpairs ? (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 4 + wpairs - 1) / wpairs) : 1;
-    auto build = [&](std::vector<WorkItem>& list, bool wide, int want) {
-      const int qr = wide ? qr_wide : qr_tile;
-      list.clear();
-      list.reserve((size_t)std::min<int64_t>((wide ? wpairs : tpairs) * want, sh.item_cap + 1));
+    if (pairs == 0) continue;
+    // Aim for about 8 items per compute unit (2 resident workgroups, several
+    // rounds in longest-first order); never split below 256 tokens.
+    int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 8 + pairs - 1) / pairs);
+    for (;;) {
+      ml.tile.clear();
+      ml.tile.reserve((size_t)std::min<int64_t>(pairs * want, sh.item_cap + 1));  // at most want pieces per pair
+      ml.merge.clear();
+      ml.partial_rows = out.decode_partials;
       for (int b = 0; b < batch; ++b) {
         const SeqInfo& s = out.seqs[b];
-        const int cols = s.qlen * G;
-        if (cols <= kDecodeCols || (cols > kTileCols) != wide) continue;
+        if (s.qlen * G <= kDecodeCols) continue;
         for (int i0 = 0; i0 < s.qlen; i0 += qr) {
           const int nq = std::min(qr, s.qlen - i0);
           const int extent = causal ? std::min(s.len, s.len - s.qlen + i0 + nq) : s.len;
@@ -335,35 +326,22 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
           for (int sp = 0; sp < ns; ++sp) {
             const int t0 = sp * chunk;
             const int t1 = std::min(extent, t0 + chunk);
-            // Cost: tile kernel ~ tiles times the 16-column blocks each of its
-            // wavefronts computes (1 for items of <= 64 columns, else 2);
-            // wide kernel ~ 32-token blocks.
-            const int cost = wide ? ceil_div(t1 - t0, 32)
-                                  : ceil_div(t1 - t0, kTileTokens) * (nq * G > kTileCols / 2 ? 2 : 1);
+            // Cost ~ tiles times the 16-column blocks each wavefront
+            // computes (1 for items of <= 64 columns, else 2).
+            const int cost = ceil_div(t1 - t0, kTileTokens) * (nq * G > kTileCols / 2 ? 2 : 1);
             for (int h = 0; h < sh.hkv; ++h)
-              list.push_back(WorkItem{b, s.qo + i0, nq, h, t0, t1, base < 0 ? -1 : base + sp * nq, cost});
+              ml.tile.push_back(WorkItem{b, s.qo + i0, nq, h, t0, t1, base < 0 ? -1 : base + sp * nq, cost});
           }
         }
       }
-    };
-    for (;;) {
-      ml.merge.clear();
-      ml.partial_rows = out.decode_partials;
-      build(ml.tile, false, want_t);
-      build(ml.wide, true, want_w);
-      if (ml.partial_rows <= slot_budget && ml.tile.size() <= (size_t)sh.item_cap &&
-          ml.wide.size() <= (size_t)sh.item_cap)
-        break;
-      if (want_t == 1 && want_w == 1) {
-        err = "attention metadata exceeds capacity: tile work lists (" + std::to_string(ml.tile.size()) + " + " +
-              std::to_string(ml.wide.size()) + " items)";
+      if (ml.partial_rows <= slot_budget && ml.tile.size() <= (size_t)sh.item_cap) break;
+      if (want == 1) {
+        err = "attention metadata exceeds capacity: tile work list (" + std::to_string(ml.tile.size()) + " items)";
         return FE_ECAPACITY;
       }
-      want_t = std::max(1, want_t / 2);
-      want_w = std::max(1, want_w / 2);
+      want = std::max(1, want / 2);
     }
-    if (!ml.tile.empty()) assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
-    if (!ml.wide.empty()) assign_shares(ml.wide, sh.wide_slots, ml.wide_off);
+    assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
   }
   for (int causal = 0; causal < 2; ++causal) {
     std::vector<MergeRow>& m = out.mode[causal].merge;

@@ -22,7 +22,6 @@ struct PlanShape {
   int num_cus = 256;        // compute units on the device (sizes split-KV)
   int decode_waves = 2048;  // wavefront slots of one decode launch
   int tile_slots = 512;     // workgroups of one tile launch (two resident per CU)
-  int wide_slots = 256;     // workgroups of one wide launch (one resident per CU)
   int item_cap = 1 << 16;   // work items per list
   int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
 };
@@ -30,8 +29,6 @@ struct PlanShape {
 struct ModeLists {
   std::vector<WorkItem> tile;            // grouped by share: share k = [tile_off[k], tile_off[k+1])
   std::vector<int32_t> tile_off;         // CSR over shares (one share per tile workgroup)
-  std::vector<WorkItem> wide;            // items of > 128 columns, grouped by share like `tile`
-  std::vector<int32_t> wide_off;         // CSR over shares (one share per wide workgroup)
   std::vector<MergeRow> merge;
   int partial_rows = 0;  // decode partials followed by this mode's tile partials
 };

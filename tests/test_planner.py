@@ -28,10 +28,7 @@ def coverage(b, causal):
         assert t0 % 16 == 0
         if kind == 1:
             assert t0 % 64 == 0
-            assert 32 < nq * b.group <= 128
-        elif kind == 2:
-            assert t0 % 64 == 0
-            assert nq * b.group <= 256 and b.qlens[seq] * b.group > 128
+            assert nq * b.group <= 128
         else:
             assert nq * b.group <= 32  # at most two 16-column MFMA blocks
         for r in range(q0, q0 + nq):
