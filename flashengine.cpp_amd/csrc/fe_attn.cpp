@@ -66,44 +66,250 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 // Decode share records: one per share the planner may cut (decode_waves / hkv).
 int share_cap(const PlanShape& sh) { return std::max(1, sh.decode_waves / sh.hkv); }
 
-// Offsets of the regions inside the metadata arena (same layout on host and device).
+// Split-KV slot budget: as many (row, all heads) partial slots as 64 MiB of
+// fp32 rows would hold; the rows are stored in 16 bits, so they take half.
+constexpr size_t kPartialBytes = 64u << 20;
+
+int partial_cap_for(int hq) {
+  return hq > 0 ? (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * sizeof(float))) : 1024;
+}
+
+// Records held by each region of a metadata arena.  A plan sizes them from
+// its capacity; the one-shot entry from the lists of the call itself (a mode
+// whose tshare region is empty is not staged).
+struct Regions {
+  size_t seqs, pages, shares, decode, tile[2], tshare[2], merge[2];
+};
+
+// Offsets of the regions inside a metadata arena (same layout on host and device).
 struct Layout {
+  Regions n;
   size_t seqs, pages, counts, dshare, decode, tile[2], tshare[2], merge[2], total;
 };
 
-Layout make_layout(const PlanShape& sh) {
+Layout make_layout(const Regions& r) {
   Layout l;
+  l.n = r;
   size_t off = 0;
   l.seqs = off;
-  off = align256(off + sizeof(SeqInfo) * sh.max_batch);
+  off = align256(off + sizeof(SeqInfo) * r.seqs);
   l.pages = off;
-  off = align256(off + sizeof(int32_t) * (size_t)sh.max_batch * sh.max_pages);
+  off = align256(off + sizeof(int32_t) * r.pages);
   l.counts = off;
   off = align256(off + sizeof(int32_t) * 8);
   l.dshare = off;
-  off = align256(off + sizeof(ShareStart) * (size_t)share_cap(sh));
+  off = align256(off + sizeof(ShareStart) * r.shares);
   l.decode = off;
-  off = align256(off + sizeof(WorkItem) * sh.item_cap);
+  off = align256(off + sizeof(DecodeItem) * r.decode);
   for (int m = 0; m < 2; ++m) {
     l.tile[m] = off;
-    off = align256(off + sizeof(WorkItem) * sh.item_cap);
+    off = align256(off + sizeof(WorkItem) * r.tile[m]);
     l.tshare[m] = off;
-    off = align256(off + sizeof(int32_t) * ((size_t)sh.tile_slots + 1));
+    off = align256(off + sizeof(int32_t) * r.tshare[m]);
   }
   for (int m = 0; m < 2; ++m) {
     l.merge[m] = off;
-    off = align256(off + sizeof(MergeRow) * sh.partial_cap);
+    off = align256(off + sizeof(MergeRow) * r.merge[m]);
   }
   l.total = off;
   return l;
 }
 
+Regions capacity_regions(const PlanShape& sh) {
+  Regions r;
+  r.seqs = (size_t)sh.max_batch;
+  r.pages = (size_t)sh.max_batch * sh.max_pages;
+  r.shares = (size_t)share_cap(sh);
+  r.decode = (size_t)sh.item_cap;
+  for (int m = 0; m < 2; ++m) {
+    r.tile[m] = (size_t)sh.item_cap;
+    r.tshare[m] = (size_t)sh.tile_slots + 1;
+    r.merge[m] = (size_t)sh.partial_cap;
+  }
+  return r;
+}
+
 // counts[] indices
 enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
 
-// Split-KV slot budget: as many (row, all heads) partial slots as 64 MiB of
-// fp32 rows would hold; the rows are stored in 16 bits, so they take half.
-constexpr size_t kPartialBytes = 64u << 20;
+// Validated shape (host-only sizes).
+int make_shape(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks, PlanShape& sh,
+               std::string& err) {
+  sh.hq = hq;
+  sh.hkv = hkv;
+  sh.dim = dim;
+  sh.page = page;
+  sh.max_batch = max_batch;
+  sh.max_pages = max_pages;
+  sh.blocks = blocks;
+  if (validate_shape(sh, err) != FE_OK) return FE_EINVAL;
+  sh.partial_cap = partial_cap_for(hq);
+  return FE_OK;
+}
+
+// Launch sizes of `device`: the work a grid of resident workgroups covers.
+int device_sizes(PlanShape& sh, int device, std::string& err) {
+  int cus = 0;
+  const hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) {
+    err = std::string("hipDeviceGetAttribute: ") + hipGetErrorString(e);
+    return FE_EDEVICE;
+  }
+  sh.num_cus = cus > 0 ? cus : 256;
+  sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
+  sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
+  return FE_OK;
+}
+
+// Writes the lists of `bp` into the host image `h` of the arena layout `l`.
+int write_image(uint8_t* h, const Layout& l, const PlanShape& sh, const BuiltPlan& bp, const int32_t* pages,
+                int npages, std::string& err) {
+  const int n_shares = (int)bp.decode_starts.size();
+  const int scap = (int)l.n.shares;
+  if (n_shares > scap) {
+    err = "attention metadata exceeds capacity: decode shares";
+    return FE_ECAPACITY;
+  }
+  std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
+  if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
+  int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
+  std::memset(cnt, 0, sizeof(int32_t) * 8);
+  cnt[kCntDecode] = n_shares;
+  // Every record up to the capacity is written: a graph launch covers them
+  // all, and records past the shares in use must read as empty.
+  std::memcpy(h + l.dshare, bp.decode_starts.data(), sizeof(ShareStart) * n_shares);
+  std::memset(h + l.dshare + sizeof(ShareStart) * n_shares, 0, sizeof(ShareStart) * (size_t)(scap - n_shares));
+  std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
+  const int tslots = sh.tile_slots;
+  for (int m = 0; m < 2; ++m) {
+    if (l.n.tshare[m] == 0) continue;  // mode not staged
+    cnt[m ? kCntTile1 : kCntTile0] = (int32_t)bp.mode[m].tile.size();
+    cnt[m ? kCntMerge1 : kCntMerge0] = (int32_t)bp.mode[m].merge.size();
+    std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
+    std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
+    // share offsets up to the launch capacity: shares past those in use are
+    // empty (a graph launch covers every slot)
+    const std::vector<int32_t>& off = bp.mode[m].tile_off;
+    const int used = off.empty() ? 0 : (int)off.size() - 1;
+    if (used > tslots) {
+      err = "attention metadata exceeds capacity: tile shares";
+      return FE_ECAPACITY;
+    }
+    int32_t* dst = reinterpret_cast<int32_t*>(h + l.tshare[m]);
+    for (int k = 0; k <= tslots; ++k) dst[k] = k <= used && !off.empty() ? off[k] : (int32_t)bp.mode[m].tile.size();
+  }
+  return FE_OK;
+}
+
+// What the kernels of one prepared plan are launched from.
+struct Launch {
+  PlanShape sh;
+  Layout lay{};
+  const uint8_t* dev = nullptr;  // metadata arena on the device
+  uint16_t* part_o = nullptr;    // 16-bit split-KV partial rows
+  float* part_lse = nullptr;
+  bool bf16 = true;
+  bool graph = false;
+  int graph_tile = -1;  // graph plans: the first graph prepare had tile work (1) or not (0)
+  int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
+  int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
+  int decode_wg = 8;         // wavefronts per decode workgroup
+  int decode_nc = 16;
+  int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
+};
+
+void init_launch(Launch& L, const PlanShape& sh, bool bf16) {
+  L.sh = sh;
+  L.bf16 = bf16;
+  L.decode_wg = decode_wg_waves(sh.hkv);
+  L.grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / L.decode_wg;  // persistent: every workgroup resident
+  L.grid_tile_cap = sh.tile_slots;
+  L.grid_merge_cap = sh.num_cus * 8;  // 4 (row, head pair) units per workgroup
+}
+
+// Launch sizes of the lists just staged.
+void record_lists(Launch& L, const BuiltPlan& bp, int nc) {
+  L.decode_nc = nc;
+  L.n_decode = (int)bp.decode_starts.size() * L.sh.hkv;  // busy decode wavefronts
+  for (int m = 0; m < 2; ++m) {
+    L.n_tile[m] = (int)bp.mode[m].tile.size();
+    L.n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
+    L.n_merge[m] = (int)bp.mode[m].merge.size();
+  }
+}
+
+int check_tensors(const void* q, const void* k_cache, const void* v_cache, const void* out, const float* lse) {
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
+    return fail(FE_EINVAL, "null tensor pointer");
+  // The kernels move q rows and K/V cache rows in 16-byte pieces (direct
+  // to LDS) and write 8-byte pieces of out.
+  const void* rows16[] = {q, k_cache, v_cache, out};
+  for (const void* ptr : rows16)
+    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+      return fail(FE_EINVAL, "attention: q, k_cache, v_cache and out must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(lse) % 4 != 0) return fail(FE_EINVAL, "attention: lse must be 4-byte aligned");
+  return FE_OK;
+}
+
+int launch_all(const Launch& L, const void* q, const void* k_cache, const void* v_cache, void* out, float* lse,
+               int causal, hipStream_t st) {
+  const int mode = causal ? 1 : 0;
+  const int32_t* counts = reinterpret_cast<const int32_t*>(L.dev + L.lay.counts);
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.kc = static_cast<const uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.seqs = reinterpret_cast<const SeqInfo*>(L.dev + L.lay.seqs);
+  a.pages = reinterpret_cast<const int32_t*>(L.dev + L.lay.pages);
+  a.part_o = L.part_o;
+  a.part_lse = L.part_lse;
+  a.hq = L.sh.hq;
+  a.hkv = L.sh.hkv;
+  a.group = L.sh.hq / L.sh.hkv;
+  int shift = 0;
+  while ((1 << shift) < L.sh.page) ++shift;
+  a.page_shift = shift;
+  a.scale_log2 = 1.4426950408889634f / 11.313708498984761f;  // log2(e) / sqrt(128)
+  hipError_t e;
+  if (L.graph || L.n_decode > 0) {
+    AttnArgs d = a;
+    d.ditems = reinterpret_cast<const DecodeItem*>(L.dev + L.lay.decode);
+    d.shares = reinterpret_cast<const ShareStart*>(L.dev + L.lay.dshare);
+    d.n_share_cap = (int)L.lay.n.shares;
+    d.n_items = counts + kCntDecode;
+    const int wv = L.decode_wg;
+    const int grid = L.graph ? L.grid_decode_cap : std::min(L.grid_decode_cap, (L.n_decode + wv - 1) / wv);
+    e = launch_decode(d, L.bf16, L.decode_wg, L.decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
+  }
+  if (L.graph ? L.graph_tile > 0 : L.n_tile[mode] > 0) {
+    AttnArgs t = a;
+    t.items = reinterpret_cast<const WorkItem*>(L.dev + L.lay.tile[mode]);
+    t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
+    t.tile_off = reinterpret_cast<const int32_t*>(L.dev + L.lay.tshare[mode]);
+    const int grid = L.graph ? L.grid_tile_cap : L.n_tshare[mode];
+    e = launch_tile(t, L.bf16, causal != 0, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "tile kernel launch");
+  }
+  if (L.graph || L.n_merge[mode] > 0) {
+    MergeArgs m{};
+    m.out = static_cast<uint16_t*>(out);
+    m.lse = lse;
+    m.rows = reinterpret_cast<const MergeRow*>(L.dev + L.lay.merge[mode]);
+    m.n_rows = counts + (mode ? kCntMerge1 : kCntMerge0);
+    m.rows_cap = (int)std::max<size_t>(1, L.lay.n.merge[mode]);
+    m.part_o = L.part_o;
+    m.part_lse = L.part_lse;
+    m.hq = L.sh.hq;
+    const int pairs4 = (int)(((int64_t)L.n_merge[mode] * ((L.sh.hq + 1) / 2) + 3) / 4);
+    const int grid = L.graph ? L.grid_merge_cap : std::min(L.grid_merge_cap, pairs4);
+    e = launch_merge(m, L.bf16, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  }
+  return FE_OK;
+}
 
 }  // namespace
 
@@ -111,12 +317,73 @@ namespace feattn {
 // Shared with the host driver (driver.cpp): sets the message returned by
 // fe_attn_last_error() on this thread and returns `code`.
 int report_error(int code, const std::string& msg) { return fail(code, msg); }
+
+// One-shot attention whose metadata arena and split-KV partials are carved
+// out of `arena` (`bytes` of device memory on `device`): plans exactly as
+// fe_attn_plan_prepare does for a plan of the same heads, page and blocks
+// (so the results are identical), stages the metadata with one copy on `st`
+// and launches as fe_attn_run does.  Allocates no device or pinned memory.
+int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const void* k_cache, const void* v_cache,
+                 void* out, float* lse, int causal, const int32_t* qo, const int32_t* kv, const int32_t* pages,
+                 const int32_t* last, int batch, int rows, int hq, int hkv, int dim, int page, int blocks, int bf16,
+                 hipStream_t st) {
+  if (batch < 0) return fail(FE_EINVAL, "batch must be non-negative");
+  if (batch > 0 && kv == nullptr) return fail(FE_EINVAL, "null metadata pointer");
+  // Capacity from the call itself: every sequence fits (the planner checks
+  // len <= (max_pages - 1) * page) and so does the page table
+  // (kv[batch] <= batch * max_pages).
+  int64_t most = 1;
+  for (int b = 0; b < batch; ++b) most = std::max<int64_t>(most, (int64_t)kv[b + 1] - kv[b]);
+  most += 1;
+  if (batch > 0) most = std::max<int64_t>(most, ((int64_t)kv[batch] + batch - 1) / batch);
+  const int max_pages = (int)std::min<int64_t>(most, INT32_MAX / 2);
+  PlanShape sh;
+  std::string err;
+  int rc = make_shape(hq, hkv, dim, page, std::max(batch, 1), max_pages, blocks, sh, err);
+  if (rc == FE_OK) rc = device_sizes(sh, device, err);
+  if (rc != FE_OK) return fail(rc, err);
+  rc = check_tensors(q, k_cache, v_cache, out, lse);
+  if (rc != FE_OK) return rc;
+  BuiltPlan bp;
+  rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
+  if (rc != FE_OK) return fail(rc, err);
+  const int mode = causal ? 1 : 0;
+  const int npages = batch > 0 ? kv[batch] : 0;
+  Regions r{};
+  r.seqs = bp.seqs.size();
+  r.pages = (size_t)npages;
+  r.shares = (size_t)share_cap(sh);
+  r.decode = bp.decode_items.size();
+  r.tile[mode] = bp.mode[mode].tile.size();
+  r.tshare[mode] = (size_t)sh.tile_slots + 1;
+  r.merge[mode] = bp.mode[mode].merge.size();
+  Launch L;
+  init_launch(L, sh, bf16 != 0);
+  L.lay = make_layout(r);
+  const size_t parts = (size_t)bp.mode[mode].partial_rows * hq;
+  const size_t o_off = L.lay.total;
+  const size_t lse_off = align256(o_off + parts * kHeadDim * sizeof(uint16_t));
+  const size_t need = lse_off + parts * sizeof(float);
+  if (need > bytes)
+    return fail(FE_ECAPACITY, "attention (no-alloc): this call needs " + std::to_string(need) +
+                                  " bytes of device scratch, more than the " + std::to_string(bytes) + " it holds");
+  std::vector<uint8_t> image(L.lay.total);
+  rc = write_image(image.data(), L.lay, sh, bp, pages, npages, err);
+  if (rc != FE_OK) return fail(rc, err);
+  // The image is pageable host memory: the copy has taken it in by the time
+  // hipMemcpyAsync returns, so it may be released right after.
+  hipError_t e = hipMemcpyAsync(arena, image.data(), L.lay.total, hipMemcpyHostToDevice, st);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(attention metadata)");
+  L.dev = arena;
+  L.part_o = reinterpret_cast<uint16_t*>(arena + o_off);
+  L.part_lse = reinterpret_cast<float*>(arena + lse_off);
+  record_lists(L, bp, bp.decode_nc);
+  return launch_all(L, q, k_cache, v_cache, out, lse, causal, st);
+}
 }  // namespace feattn
 
 struct fe_attn_plan {
-  PlanShape sh;
-  bool bf16 = true;
-  Layout lay{};
+  Launch run;                  // arena pointers, shape and launch sizes
   uint8_t* dev = nullptr;      // metadata arena
   uint8_t* host = nullptr;     // pinned mirror
   uint16_t* part_o = nullptr;  // 16-bit partial rows
@@ -124,16 +391,8 @@ struct fe_attn_plan {
   hipEvent_t staged = nullptr;
   bool staged_pending = false;
   int device = 0;
-  // state of the last prepare
   bool prepared = false;
-  bool graph = false;
-  int graph_nc = 0;
-  int graph_tile = -1;  // the first graph prepare had tile work (1) or not (0)
-  int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
-  int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
-  int decode_wg = 8;  // wavefronts per decode workgroup
-  int decode_nc = 16;
-  int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
+  int graph_nc = 0;  // graph plans: the decode column variant of the first graph prepare
 };
 
 extern "C" {
@@ -147,46 +406,29 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (plan_out == nullptr) return fail(FE_EINVAL, "plan_out is null");
   *plan_out = nullptr;
   PlanShape sh;
-  sh.hq = hq;
-  sh.hkv = hkv;
-  sh.dim = dim;
-  sh.page = page;
-  sh.max_batch = max_batch;
-  sh.max_pages = max_pages;
-  sh.blocks = blocks;
   std::string err;
-  if (validate_shape(sh, err) != FE_OK) return fail(FE_EINVAL, err);
-  const size_t slot_bytes = (size_t)hq * (kHeadDim + 1) * sizeof(float);
-  sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / slot_bytes);
-
+  int rc = make_shape(hq, hkv, dim, page, max_batch, max_pages, blocks, sh, err);
+  if (rc != FE_OK) return fail(rc, err);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
-  sh.num_cus = cus > 0 ? cus : 256;
+  rc = device_sizes(sh, dev, err);
+  if (rc != FE_OK) return fail(rc, err);
 
-  sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
-  sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
   auto* p = new (std::nothrow) fe_attn_plan();
   if (p == nullptr) return fail(FE_ENOMEM, "out of host memory");
-  p->sh = sh;
-  p->bf16 = bf16 != 0;
   p->device = dev;
-  p->lay = make_layout(sh);
-  p->decode_wg = decode_wg_waves(hkv);
-  p->grid_decode_cap = sh.num_cus * kDecodeWavesPerCu / p->decode_wg;  // persistent: every workgroup resident
-  p->grid_tile_cap = sh.tile_slots;
-  p->grid_merge_cap = sh.num_cus * 8;   // 4 (row, head pair) units per workgroup
+  init_launch(p->run, sh, bf16 != 0);
+  p->run.lay = make_layout(capacity_regions(sh));
+  const size_t total = p->run.lay.total;
   auto cleanup = [&](int code, const std::string& msg) {
     fe_attn_plan_destroy(p);
     return fail(code, msg);
   };
-  if (hipMalloc(&p->dev, p->lay.total) != hipSuccess) return cleanup(FE_ENOMEM, "hipMalloc(plan metadata) failed");
-  if (hipHostMalloc(&p->host, p->lay.total, hipHostMallocDefault) != hipSuccess)
+  if (hipMalloc(&p->dev, total) != hipSuccess) return cleanup(FE_ENOMEM, "hipMalloc(plan metadata) failed");
+  if (hipHostMalloc(&p->host, total, hipHostMallocDefault) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipHostMalloc(plan staging) failed");
-  std::memset(p->host, 0, p->lay.total);
+  std::memset(p->host, 0, total);
   if (hipMalloc(&p->part_o, (size_t)sh.partial_cap * hq * kHeadDim * sizeof(uint16_t)) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipMalloc(split-KV partials) failed");
   if (hipMalloc(&p->part_lse, (size_t)sh.partial_cap * hq * sizeof(float)) != hipSuccess)
@@ -194,8 +436,11 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
   if (hipEventCreateWithFlags(&p->staged, hipEventDisableTiming) != hipSuccess)
     return cleanup(FE_EDEVICE, "hipEventCreate failed");
   // Counts start at zero so a run before any prepare does nothing.
-  if (hipMemset(p->dev, 0, p->lay.total) != hipSuccess) return cleanup(FE_EDEVICE, "hipMemset(plan) failed");
+  if (hipMemset(p->dev, 0, total) != hipSuccess) return cleanup(FE_EDEVICE, "hipMemset(plan) failed");
   if (hipDeviceSynchronize() != hipSuccess) return cleanup(FE_EDEVICE, "hipDeviceSynchronize failed");
+  p->run.dev = p->dev;
+  p->run.part_o = p->part_o;
+  p->run.part_lse = p->part_lse;
   *plan_out = p;
   return FE_OK;
 }
@@ -215,12 +460,13 @@ int fe_attn_plan_destroy(fe_attn_plan* p) {
 int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, const int32_t* pages,
                          const int32_t* last, int batch, int rows, int graph, void* stream) {
   if (p == nullptr) return fail(FE_EINVAL, "plan is null");
+  Launch& L = p->run;
   BuiltPlan bp;
   std::string err;
-  const int rc = build_plan(p->sh, qo, kv, pages, last, batch, rows, bp, err);
+  const int rc = build_plan(L.sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   int nc = bp.decode_nc;
-  int graph_nc = p->graph_nc, graph_tile = p->graph_tile;
+  int graph_nc = p->graph_nc, graph_tile = L.graph_tile;
   if (graph) {
     // Captured launches bake in the decode column variant; a later prepare
     // may not need a wider one (the reference refuses layout changes under
@@ -246,37 +492,10 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
     p->staged_pending = false;
   }
-  const Layout& l = p->lay;
+  const Layout& l = L.lay;
   uint8_t* h = p->host;
   const int npages = batch > 0 ? kv[batch] : 0;
-  std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
-  if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
-  int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
-  const int n_shares = (int)bp.decode_starts.size();
-  const int scap = share_cap(p->sh);
-  if (n_shares > scap) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: decode shares");
-  cnt[kCntDecode] = n_shares;
-  // Every record up to the capacity is written: a graph launch covers them
-  // all, and records past the shares in use must read as empty.
-  std::memcpy(h + l.dshare, bp.decode_starts.data(), sizeof(ShareStart) * n_shares);
-  std::memset(h + l.dshare + sizeof(ShareStart) * n_shares, 0, sizeof(ShareStart) * (size_t)(scap - n_shares));
-  cnt[kCntTile0] = (int32_t)bp.mode[0].tile.size();
-  cnt[kCntTile1] = (int32_t)bp.mode[1].tile.size();
-  cnt[kCntMerge0] = (int32_t)bp.mode[0].merge.size();
-  cnt[kCntMerge1] = (int32_t)bp.mode[1].merge.size();
-  std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
-  const int tslots = p->sh.tile_slots;
-  for (int m = 0; m < 2; ++m) {
-    std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
-    std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
-    // share offsets up to the launch capacity: shares past those in use are
-    // empty (a graph launch covers every slot)
-    const std::vector<int32_t>& off = bp.mode[m].tile_off;
-    const int used = off.empty() ? 0 : (int)off.size() - 1;
-    if (used > tslots) return fail(FE_ECAPACITY, "attention metadata exceeds capacity: tile shares");
-    int32_t* dst = reinterpret_cast<int32_t*>(h + l.tshare[m]);
-    for (int k = 0; k <= tslots; ++k) dst[k] = k <= used && !off.empty() ? off[k] : (int32_t)bp.mode[m].tile.size();
-  }
+  if (write_image(h, l, L.sh, bp, pages, npages, err) != FE_OK) return fail(FE_ECAPACITY, err);
   auto copy = [&](size_t off, size_t bytes) -> hipError_t {
     if (bytes == 0) return hipSuccess;
     return hipMemcpyAsync(p->dev + off, h + off, bytes, hipMemcpyHostToDevice, st);
@@ -285,11 +504,11 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e == hipSuccess) e = copy(l.seqs, sizeof(SeqInfo) * bp.seqs.size());
   if (e == hipSuccess) e = copy(l.pages, sizeof(int32_t) * npages);
   if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
-  if (e == hipSuccess) e = copy(l.dshare, sizeof(ShareStart) * (size_t)scap);
+  if (e == hipSuccess) e = copy(l.dshare, sizeof(ShareStart) * l.n.shares);
   if (e == hipSuccess) e = copy(l.decode, sizeof(DecodeItem) * bp.decode_items.size());
   for (int m = 0; m < 2 && e == hipSuccess; ++m) {
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
-    if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * ((size_t)tslots + 1));
+    if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * l.n.tshare[m]);
     if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
   }
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
@@ -297,18 +516,12 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
   p->staged_pending = true;
   p->prepared = true;
-  p->graph = graph != 0;
+  L.graph = graph != 0;
   if (graph) {
     p->graph_nc = graph_nc;
-    p->graph_tile = graph_tile;
+    L.graph_tile = graph_tile;
   }
-  p->decode_nc = nc;
-  p->n_decode = n_shares * p->sh.hkv;  // busy decode wavefronts
-  for (int m = 0; m < 2; ++m) {
-    p->n_tile[m] = (int)bp.mode[m].tile.size();
-    p->n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
-    p->n_merge[m] = (int)bp.mode[m].merge.size();
-  }
+  record_lists(L, bp, nc);
   return FE_OK;
 }
 
@@ -316,72 +529,9 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
                 int causal, void* stream) {
   if (p == nullptr) return fail(FE_EINVAL, "plan is null");
   if (!p->prepared) return fail(FE_EINVAL, "attention called before prepare_plan");
-  if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
-    return fail(FE_EINVAL, "null tensor pointer");
-  // The kernels move q rows and K/V cache rows in 16-byte pieces (direct
-  // to LDS) and write 8-byte pieces of out.
-  const void* rows16[] = {q, k_cache, v_cache, out};
-  for (const void* ptr : rows16)
-    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
-      return fail(FE_EINVAL, "attention: q, k_cache, v_cache and out must be 16-byte aligned");
-  if (reinterpret_cast<uintptr_t>(lse) % 4 != 0) return fail(FE_EINVAL, "attention: lse must be 4-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mode = causal ? 1 : 0;
-  const int32_t* counts = reinterpret_cast<const int32_t*>(p->dev + p->lay.counts);
-  AttnArgs a{};
-  a.q = static_cast<const uint16_t*>(q);
-  a.kc = static_cast<const uint16_t*>(k_cache);
-  a.vc = static_cast<const uint16_t*>(v_cache);
-  a.out = static_cast<uint16_t*>(out);
-  a.lse = lse;
-  a.seqs = reinterpret_cast<const SeqInfo*>(p->dev + p->lay.seqs);
-  a.pages = reinterpret_cast<const int32_t*>(p->dev + p->lay.pages);
-  a.part_o = p->part_o;
-  a.part_lse = p->part_lse;
-  a.hq = p->sh.hq;
-  a.hkv = p->sh.hkv;
-  a.group = p->sh.hq / p->sh.hkv;
-  int shift = 0;
-  while ((1 << shift) < p->sh.page) ++shift;
-  a.page_shift = shift;
-  a.scale_log2 = 1.4426950408889634f / 11.313708498984761f;  // log2(e) / sqrt(128)
-  hipError_t e;
-  if (p->graph || p->n_decode > 0) {
-    AttnArgs d = a;
-    d.ditems = reinterpret_cast<const DecodeItem*>(p->dev + p->lay.decode);
-    d.shares = reinterpret_cast<const ShareStart*>(p->dev + p->lay.dshare);
-    d.n_share_cap = share_cap(p->sh);
-    d.n_items = counts + kCntDecode;
-    const int wv = p->decode_wg;
-    const int grid = p->graph ? p->grid_decode_cap : std::min(p->grid_decode_cap, (p->n_decode + wv - 1) / wv);
-    e = launch_decode(d, p->bf16, p->decode_wg, p->decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
-    if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
-  }
-  if (p->graph ? p->graph_tile > 0 : p->n_tile[mode] > 0) {
-    AttnArgs t = a;
-    t.items = reinterpret_cast<const WorkItem*>(p->dev + p->lay.tile[mode]);
-    t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
-    t.tile_off = reinterpret_cast<const int32_t*>(p->dev + p->lay.tshare[mode]);
-    const int grid = p->graph ? p->grid_tile_cap : p->n_tshare[mode];
-    e = launch_tile(t, p->bf16, causal != 0, std::max(grid, 1), st);
-    if (e != hipSuccess) return hip_fail(e, "tile kernel launch");
-  }
-  if (p->graph || p->n_merge[mode] > 0) {
-    MergeArgs m{};
-    m.out = static_cast<uint16_t*>(out);
-    m.lse = lse;
-    m.rows = reinterpret_cast<const MergeRow*>(p->dev + p->lay.merge[mode]);
-    m.n_rows = counts + (mode ? kCntMerge1 : kCntMerge0);
-    m.rows_cap = p->sh.partial_cap;
-    m.part_o = p->part_o;
-    m.part_lse = p->part_lse;
-    m.hq = p->sh.hq;
-    const int pairs4 = (int)(((int64_t)p->n_merge[mode] * ((p->sh.hq + 1) / 2) + 3) / 4);
-    const int grid = p->graph ? p->grid_merge_cap : std::min(p->grid_merge_cap, pairs4);
-    e = launch_merge(m, p->bf16, std::max(grid, 1), st);
-    if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
-  }
-  return FE_OK;
+  const int rc = check_tensors(q, k_cache, v_cache, out, lse);
+  if (rc != FE_OK) return rc;
+  return launch_all(p->run, q, k_cache, v_cache, out, lse, causal, static_cast<hipStream_t>(stream));
 }
 
 int fe_rope_table(float* table, int max_len, int dim, double theta, void* stream) {
@@ -492,7 +642,7 @@ int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int
   sh.max_batch = max_batch;
   sh.max_pages = max_pages;
   sh.blocks = blocks;
-  if (hq > 0) sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * 4));
+  sh.partial_cap = partial_cap_for(hq);
   BuiltPlan bp;
   std::string err;
   const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
@@ -517,7 +667,7 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch, int max
   sh.max_batch = max_batch;
   sh.max_pages = max_pages;
   sh.blocks = blocks;
-  if (hq > 0) sh.partial_cap = (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * 4));
+  sh.partial_cap = partial_cap_for(hq);
   BuiltPlan bp;
   std::string err;
   const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);

@@ -39,6 +39,7 @@ C_SYMBOLS = (
     "fe_attn_plan_describe",
     "fe_attn_plan_dump",
     "fe_attn_version",
+    "fe_attn_run_noalloc",
 )
 
 # Every extern "C" symbol of include/fe_driver.h.
@@ -90,6 +91,7 @@ def lib() -> ctypes.CDLL:
     L.fe_attn_plan_destroy.argtypes = [_vp]
     L.fe_attn_plan_prepare.argtypes = [_vp, _i32p, _i32p, _i32p, _i32p, _int, _int, _int, _vp]
     L.fe_attn_run.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
+    L.fe_attn_run_noalloc.argtypes = [_vp] * 5 + [_int] + [_i32p] * 4 + [_int] * 8 + [_vp]
     L.fe_rope.argtypes = [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _int]
     L.fe_store.argtypes = [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _int]
     L.fe_rope_append.argtypes = [_vp] * 8 + [_int] * 7 + [_vp]
@@ -187,6 +189,17 @@ class Plan:
             self.close()
         except Exception:
             pass
+
+
+def run_noalloc(q, k_cache, v_cache, out, qo: Sequence[int], kv: Sequence[int], pages: Sequence[int],
+                last: Sequence[int], batch: int, rows: int, hq: int, hkv: int, dim: int, page: int,
+                blocks: int, bf16: bool, causal: bool = True, lse=None, stream=None) -> None:
+    """Plan-free attention that allocates no device memory (fe_attn_run_noalloc):
+    the results of Plan(...).prepare(...) followed by run(...)."""
+    _check(lib().fe_attn_run_noalloc(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(lse),
+                                     int(bool(causal)), _i32(qo), _i32(kv), _i32(pages), _i32(last),
+                                     batch, rows, hq, hkv, dim, page, blocks, int(bool(bf16)),
+                                     _stream(stream)))
 
 
 def rope(q, k, pos, cache, rows: int, hq: int, hkv: int, dim: int, bf16: bool,
