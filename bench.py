@@ -40,8 +40,9 @@ def log(*a):
 
 def measured_traffic():
     """HBM bytes per decode step (decode kernel + split-KV merge) from the
-    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload,
-    calibrated against a 1 GiB copy; None if the summary is absent."""
+    committed rocprofv3 summary of this workload: DRAM read and write
+    request counters summed over every channel, used raw (no calibration
+    factor); None if the summary is absent."""
     path = os.path.join(ROOT, "profiles", "decode_qwen3_8b_hbm_traffic.txt")
     if not os.path.exists(path):
         return None
@@ -299,8 +300,9 @@ def _long(dev, res):
 
 def copy_calibration(dev, mib=1024):
     """A plain device copy of known size (read + write of `mib` MiB), timed:
-    the practical bandwidth reference, and the kernel whose FETCH_SIZE /
-    WRITE_SIZE counters calibrate the attention kernels' traffic."""
+    the practical bandwidth reference, and the kernel on which the DRAM
+    request counters' byte formulas are checked (exactly `mib` MiB read and
+    written)."""
     import torch
 
     n = mib << 20
@@ -311,37 +313,78 @@ def copy_calibration(dev, mib=1024):
     return {"bytes_per_copy": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / ms / 1e6, 1)}
 
 
-def cpu_baseline(b):
-    """Oracle (LibTorch-CPU restatement of the reference ATen attention) on
-    the full decode batch: median of 3 after 1 warmup."""
+def host_cpu():
+    """The host the CPU baseline runs on: model name from /proc/cpuinfo, the
+    CPUs this process may run on (what `nproc` reports), os.cpu_count() and
+    OMP_NUM_THREADS."""
+    model = platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return {"model": model, "nproc": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count(),
+            "omp_num_threads": int(omp) if omp and omp.isdigit() else None}
+
+
+def oracle_time(b, q, kc, vc, causal, runs=4):
+    """Median wall time of the oracle's prepare_plan and attention over
+    runs - 1 calls after one warm-up call."""
     import torch
 
-    from feattn import workloads as W
     from oracle import aten_attention as A
 
-    q, kc, vc = W.make_tensors(b, seed=7)
     times, prep = [], []
-    for it in range(4):
+    for it in range(runs):
         t0 = time.perf_counter()
         p = A.create_plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
         A.prepare_plan(p, b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
         t1 = time.perf_counter()
         out = torch.empty_like(q)
-        A.attention(p, q, kc, vc, out, True)
+        A.attention(p, q, kc, vc, out, causal)
         t2 = time.perf_counter()
         if it:
             prep.append(t1 - t0)
             times.append(t2 - t1)
         log(f"cpu baseline run {it}: prepare {t1 - t0:.3f}s attention {t2 - t1:.3f}s")
-    t = statistics.median(times)
+    return statistics.median(times), statistics.median(prep)
+
+
+def cpu_baseline(b):
+    """Oracle (LibTorch-CPU restatement of the reference ATen attention,
+    sequence by sequence) on the full decode batch and on the full chunked
+    prefill batch: median of 3 after 1 warm-up each, with as many threads as
+    this process may use (nproc, capped by OMP_NUM_THREADS when set)."""
+    import torch
+
+    from feattn import workloads as W
+
+    host = host_cpu()
+    threads = host["nproc"]
+    if host["omp_num_threads"]:
+        threads = min(threads, host["omp_num_threads"])
+    torch.set_num_threads(threads)
+    q, kc, vc = W.make_tensors(b, seed=7)
+    t, tp = oracle_time(b, q, kc, vc, True)
+    pb = W.qwen3_8b_prefill()
+    pq, pkc, pvc = W.make_tensors(pb, seed=8)
+    pt, ptp = oracle_time(pb, pq, pkc, pvc, True)
+    pflops = W.attention_flops(pb, True)
     return {
         "value": round(W.decode_bytes(b) / t / 1e9, 3), "unit": "GB/s",
         "cores": torch.get_num_threads(), "kind": "port",
         "sample": "full 64-sequence decode batch (same metadata, seeded bf16 inputs); "
                   "LibTorch-CPU restatement of src/portable_gpu_ops.cpp attention; median of 3 "
                   "after 1 warmup",
-        "attention_s": round(t, 4), "prepare_plan_s": round(statistics.median(prep), 4),
-        "cpu": platform.processor() or platform.machine(), "torch": torch.__version__}
+        "attention_s": round(t, 4), "prepare_plan_s": round(tp, 4),
+        "prefill": {"value": round(pflops / pt / 1e9, 2), "unit": "GFLOP/s",
+                    "sample": "full chunked prefill batch (8 seqs, 8192 query rows, causal), the "
+                              "same restatement, sequence by sequence; median of 3 after 1 warmup",
+                    "attention_s": round(pt, 4), "prepare_plan_s": round(ptp, 4)},
+        "cpu": host, "torch": torch.__version__}
 
 
 def main():
@@ -396,7 +439,8 @@ def main():
                      "algorithmic_bytes": nbytes,
                      "timed": "one fe_attn_run per step (attn_decode_kernel + attn_merge_kernel, "
                               "the whole attention call), HIP events on the launch stream; traffic "
-                              "from profiles/decode_qwen3_8b_hbm_traffic.txt"},
+                              "= DRAM read + write request counters of both kernels, "
+                              "profiles/decode_qwen3_8b_hbm_traffic.txt"},
         "cpu_baseline": cpu,
         "secondary": sec,
     }
