@@ -31,6 +31,8 @@ std::vector<int64_t> cut_uniform(int64_t stream, int64_t quota) {
   return cuts;
 }
 
+}  // namespace
+
 // Assigns items to `slots` shares (one per tile workgroup) by the longest
 // processing time rule -- in decreasing cost order, each item goes to the
 // least-loaded share -- and regroups them share by share (longest first
@@ -84,8 +86,6 @@ void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>
   for (size_t i = 0; i < items.size(); ++i) grouped[pos[share[i]]++] = items[i];
   items.swap(grouped);
 }
-
-}  // namespace
 
 int validate_shape(const PlanShape& sh, std::string& err) {
   if (sh.dim != kHeadDim) {

@@ -45,6 +45,12 @@ struct BuiltPlan {
   ModeLists mode[2];             // [0] full (non-causal), [1] causal
 };
 
+// Longest-processing-time assignment of items (by `cost`, >= 0) to at most
+// `slots` (< 2^20) shares: items in decreasing cost order (ties keep their
+// order) each go to the least-loaded share, the lowest index among equals;
+// `items` is regrouped share by share and `off` gets the CSR offsets.
+void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off);
+
 // Returns 0 (FE_OK) or a negative FE_E* code with `err` set.
 int validate_shape(const PlanShape& sh, std::string& err);
 int build_plan(const PlanShape& sh, const int32_t* qo, const int32_t* kv, const int32_t* pages,

@@ -40,6 +40,7 @@ C_SYMBOLS = (
     "fe_attn_plan_dump",
     "fe_attn_version",
     "fe_attn_run_noalloc",
+    "fe_attn_assign_shares",
 )
 
 # Every extern "C" symbol of include/fe_driver.h.
@@ -92,6 +93,7 @@ def lib() -> ctypes.CDLL:
     L.fe_attn_plan_prepare.argtypes = [_vp, _i32p, _i32p, _i32p, _i32p, _int, _int, _int, _vp]
     L.fe_attn_run.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
     L.fe_attn_run_noalloc.argtypes = [_vp] * 5 + [_int] + [_i32p] * 4 + [_int] * 8 + [_vp]
+    L.fe_attn_assign_shares.argtypes = [_i32p, _int, _int, _i32p, _i32p, ctypes.POINTER(_int)]
     L.fe_rope.argtypes = [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _int]
     L.fe_store.argtypes = [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _int]
     L.fe_rope_append.argtypes = [_vp] * 8 + [_int] * 7 + [_vp]
@@ -230,6 +232,17 @@ def describe(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, la
     _check(lib().fe_attn_plan_describe(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
                                        _i32(kv), _i32(pages), _i32(last), batch, rows, out))
     return tuple(out)
+
+
+def assign_shares(costs: Sequence[int], slots: int):
+    """Host-only planner share assignment: (order, off) -- the input index of
+    each item share by share, and the CSR offsets of the shares."""
+    n = len(costs)
+    order = (ctypes.c_int32 * max(1, n))()
+    off = (ctypes.c_int32 * (min(slots, n) + 2))()
+    ns = _int()
+    _check(lib().fe_attn_assign_shares(_i32(costs), n, slots, order, off, ctypes.byref(ns)))
+    return list(order[:n]), list(off[:ns.value + 1])
 
 
 def dump(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, last, batch, rows,

@@ -160,6 +160,18 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch,
                       const int32_t* last, int batch, int rows, int causal,
                       int32_t* items_out, int cap, int* n_out);
 
+/* Host-only: the share assignment fe_attn_plan_prepare gives tile items
+ * (one share per tile workgroup), on caller-chosen costs, for tests.  Longest
+ * processing time: items in decreasing cost order (equal costs keep their
+ * input order) each go to the least-loaded share, the lowest index among
+ * equals.  costs[n] >= 0, total below 2^43, 1 <= slots < 2^20.  Writes
+ * order_out[n] (input index of each item, share by share) and
+ * off_out[0..*n_shares_out] (CSR offsets of the max(1, min(slots, n))
+ * shares; off_out must hold min(slots, n) + 2 entries). */
+int fe_attn_assign_shares(const int32_t* costs, int n, int slots,
+                          int32_t* order_out, int32_t* off_out,
+                          int* n_shares_out);
+
 /* Library identification, e.g. "feattn-hip-gfx950 <version>". */
 const char* fe_attn_version(void);
 

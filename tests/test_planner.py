@@ -120,3 +120,62 @@ def test_empty_batch_and_zero_row_sequence():
     b = W.make_batch(32, 8, starts=[20, 7], qlens=[0, 2], seed=2)
     items = coverage(b, True)
     assert all(it[1] == 1 for it in items)
+
+
+def lpt_reference(costs, slots):
+    """Longest processing time, stated directly: items in decreasing cost
+    order (ties in input order), each to the least-loaded share (lowest index
+    among equals); then grouped share by share in that order."""
+    n = len(costs)
+    m = max(1, min(slots, n))
+    order = sorted(range(n), key=lambda i: -costs[i])  # sorted() is stable
+    loads, share = [0] * m, {}
+    for i in order:
+        k = min(range(m), key=lambda s: (loads[s], s))
+        share[i] = k
+        loads[k] += costs[i]
+    grouped = [i for k in range(m) for i in order if share[i] == k]
+    off = [0]
+    for k in range(m):
+        off.append(off[-1] + sum(1 for i in order if share[i] == k))
+    return grouped, off, loads
+
+
+@pytest.mark.parametrize("case", ["random", "tied", "over_65536", "few_items", "empty"])
+def test_share_assignment_matches_lpt_rule(case):
+    """The planner's tile-share assignment (counting sort for costs <= 65536,
+    comparison sort above) against the rule stated in Python."""
+    rng = np.random.default_rng(11)
+    slots = 512
+    if case == "random":
+        costs = rng.integers(1, 400, size=3000).tolist()
+    elif case == "tied":
+        costs = rng.choice([4, 8, 8, 16], size=2000).tolist()
+    elif case == "over_65536":
+        costs = rng.integers(1, 400, size=1500).tolist() + [70000, 65537, 1 << 20]
+        rng.shuffle(costs)
+    elif case == "few_items":
+        costs, slots = [5, 3, 5, 1], 16
+    else:
+        costs = []
+    order, off = feattn.assign_shares(costs, slots)
+    want_order, want_off, loads = lpt_reference(costs, slots)
+    assert order == want_order
+    assert off == want_off
+    # the ranges split the list exactly, one per share, at most `slots` of them
+    assert off[0] == 0 and off[-1] == len(costs) and all(a <= b for a, b in zip(off, off[1:]))
+    assert len(off) - 1 <= max(1, min(slots, len(costs)))
+    assert sorted(order) == list(range(len(costs)))
+    # longest first inside each share
+    for k in range(len(off) - 1):
+        c = [costs[i] for i in order[off[k]:off[k + 1]]]
+        assert c == sorted(c, reverse=True)
+    if costs and case != "over_65536":
+        assert max(loads) <= sum(costs) / min(slots, len(costs)) + max(costs)  # the LPT bound
+
+
+def test_share_assignment_rejects_bad_input():
+    with pytest.raises(RuntimeError, match="negative cost"):
+        feattn.assign_shares([3, -1], 4)
+    with pytest.raises(RuntimeError, match="slots"):
+        feattn.assign_shares([3], 0)
