@@ -127,3 +127,17 @@ def test_exact_counts_head_layouts(dev, hq, hkv):
     b = W.make_batch(hq, hkv, starts=[4095, 0, 777, 5000, 31], qlens=[1, 1, 1, 2, 90], seed=hq + hkv,
                      extra_pages=1)
     run_case(dev, b, True, "f16")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (32, 4), (24, 6)])
+def test_exact_counts_short_blocks(dev, causal, hq, hkv):
+    """Blocks of rows just past the decode kernel's 32 columns per kv head
+    (one to two decode widths: DFlash and verify blocks, on the tile kernel),
+    with both masks, next to single decode rows and a longer chunk."""
+    G = hq // hkv
+    rmax = 32 // G
+    b = W.make_batch(hq, hkv, starts=[5000, 900, 3000, 17, 40, 12000, 100],
+                     qlens=[1, rmax + 1, 2 * rmax, 2 * rmax, 1, rmax + 2, 300], seed=hq * hkv,
+                     extra_pages=2)
+    run_case(dev, b, causal, "f16")
