@@ -1,8 +1,8 @@
 // Attention entry point that allocates nothing: plan metadata and split-KV
 // partials live in a fixed device array of this library instead of memory
 // that fe_attn_plan_create allocates.  For callers that may not allocate
-// device memory (code under HIP graph capture, serving loops and harnesses
-// that forbid hipMalloc).
+// device memory (serving loops and harnesses that forbid hipMalloc).  Not
+// capturable: each call copies its work lists from host memory it releases.
 #include <hip/hip_runtime.h>
 
 #include <atomic>

@@ -117,18 +117,19 @@ int fe_rope_append(void* q, const void* k, const void* v, void* k_cache,
                    int bf16, int max_positions, int cache_slots, void* stream);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
- * memory (code under HIP graph capture, serving loops and harnesses that
- * forbid hipMalloc): fe_attn_plan_prepare + fe_attn_run in one call, without
- * a plan.  Same arguments and results as a plan of (hq, hkv, dim, page,
+ * memory (serving loops and harnesses that forbid hipMalloc):
+ * fe_attn_plan_prepare + fe_attn_run in one call, without a plan.  Same arguments and results as a plan of (hq, hkv, dim, page,
  * blocks, bf16) prepared with (qo, kv, pages, last, batch, rows) and run
  * with (q, k_cache, v_cache, out, lse, causal): the same work lists, kernels
  * and bits.  The work lists and split-KV partials live in a 48 MiB device
  * array of the library (one per device, kept until the process ends); a
  * call that needs more returns FE_ECAPACITY.  Allocates no device or pinned
  * memory; the metadata goes to the device by one copy from pageable host
- * memory on `stream`.  Every call on a device shares that device's array:
- * calls that overlap on one device (other streams, other threads) race, and
- * calls ordered on one stream do not. */
+ * memory on `stream`, so the call must not be captured into a HIP graph (a
+ * replay would copy from host memory the call has released; capture the
+ * plan entry points instead).  Every call on a device shares that device's
+ * array: calls that overlap on one device (other streams, other threads)
+ * race, and calls ordered on one stream do not. */
 int fe_attn_run_noalloc(const void* q, const void* k_cache, const void* v_cache,
                         void* out, float* lse, int causal, const int32_t* qo,
                         const int32_t* kv, const int32_t* pages,
