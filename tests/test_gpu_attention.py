@@ -79,6 +79,11 @@ CASES = [
     (40, 8, [60, 250], [1, 90]),                             # GQA 5 (non power of two)
     (16, 2, [1000, 5, 300, 64], [1, 1, 3, 1]),               # hkv 2: 2-wavefront decode workgroups
     (24, 6, [2000, 17, 90, 4000], [1, 2, 40, 1]),            # hkv 6: 2-wavefront decode workgroups
+    (24, 8, [700, 2000, 33, 5], [1, 10, 11, 50]),            # GQA 3: 30-column decode items, 33-column tile items
+    (48, 8, [900, 17, 3000], [5, 6, 1]),                     # GQA 6
+    (128, 8, [1000, 64, 2500], [2, 3, 1]),                   # GQA 16: 2 rows fill a decode item
+    (64, 2, [1500, 40], [1, 2]),                             # GQA 32
+    (128, 1, [800, 20], [1, 2]),                             # GQA 128: one row is a whole tile item
 ]
 
 
