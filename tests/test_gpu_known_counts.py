@@ -144,3 +144,14 @@ def test_exact_counts_short_blocks(dev, causal, hq, hkv):
                      qlens=[1, rmax + 1, 2 * rmax, 2 * rmax, 1, rmax + 2, 300], seed=hq * hkv,
                      extra_pages=2)
     run_case(dev, b, causal, "f16")
+
+
+@pytest.mark.parametrize("page", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_exact_counts_page_sizes(dev, page, causal):
+    """Larger pages: lengths ending just before, on and just after page
+    boundaries, decode rows and chunks, so every page-index shift and the
+    last partial page are pinned exactly."""
+    b = W.make_batch(32, 8, starts=[page - 2, page - 1, page, 3 * page + 1, 5000, 700],
+                     qlens=[1, 1, 1, 2, 1, 100], seed=page, page=page, extra_pages=2)
+    run_case(dev, b, causal, "f16")
