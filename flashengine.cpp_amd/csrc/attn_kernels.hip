@@ -711,7 +711,7 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
 // ===========================================================================
 // One wavefront per (merged row, pair of heads): lanes 0-31 take head 2hp,
 // lanes 32-63 head 2hp + 1, each lane 4 of the 128 dims, so every partial-row
-// load is one 16-byte access per lane.  Splits are folded in batches of
+// load is one 8-byte access per lane.  Splits are folded in batches of
 // kMergeBatch whose log-sum-exps and partial rows are all in flight
 // together; loads past a row's split count are not issued.
 template <bool BF16>
