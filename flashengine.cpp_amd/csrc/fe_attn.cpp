@@ -370,8 +370,9 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   std::vector<uint8_t> image(L.lay.total);
   rc = write_image(image.data(), L.lay, sh, bp, pages, npages, err);
   if (rc != FE_OK) return fail(rc, err);
-  // The image is pageable host memory: the copy has taken it in by the time
-  // hipMemcpyAsync returns, so it may be released right after.
+  // The image is pageable host memory, which HIP copies synchronously (the
+  // call returns once the copy has run on `st`), so it may be released right
+  // after.
   hipError_t e = hipMemcpyAsync(arena, image.data(), L.lay.total, hipMemcpyHostToDevice, st);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(attention metadata)");
   L.dev = arena;

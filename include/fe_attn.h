@@ -125,7 +125,9 @@ int fe_rope_append(void* q, const void* k, const void* v, void* k_cache,
  * array of the library (one per device, kept until the process ends); a
  * call that needs more returns FE_ECAPACITY.  Allocates no device or pinned
  * memory; the metadata goes to the device by one copy from pageable host
- * memory on `stream`, so the call must not be captured into a HIP graph (a
+ * memory on `stream`, which HIP performs synchronously: the call returns
+ * after the stream's earlier work and the copy have run.  For the same
+ * reason the call must not be captured into a HIP graph (a
  * replay would copy from host memory the call has released; capture the
  * plan entry points instead).  Every call on a device shares that device's
  * array: calls that overlap on one device (other streams, other threads)
