@@ -367,6 +367,10 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   if (need > bytes)
     return fail(FE_ECAPACITY, "attention (no-alloc): this call needs " + std::to_string(need) +
                                   " bytes of device scratch, more than the " + std::to_string(bytes) + " it holds");
+  // Nothing in the arena has to start at zero, whatever an earlier call
+  // left there: the copy below writes every metadata field the kernels read
+  // (counts, share records, lists), and every partial slot a merge reads is
+  // written by this call's decode or tile kernel first.
   std::vector<uint8_t> image(L.lay.total);
   rc = write_image(image.data(), L.lay, sh, bp, pages, npages, err);
   if (rc != FE_OK) return fail(rc, err);
