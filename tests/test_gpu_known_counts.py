@@ -155,3 +155,16 @@ def test_exact_counts_page_sizes(dev, page, causal):
     b = W.make_batch(32, 8, starts=[page - 2, page - 1, page, 3 * page + 1, 5000, 700],
                      qlens=[1, 1, 1, 2, 1, 100], seed=page, page=page, extra_pages=2)
     run_case(dev, b, causal, "f16")
+
+
+def test_counts_single_128k_sequence(dev):
+    """One 131072-token decode row (and a 6-token one) spread over every
+    decode share: about 256 pieces whose partials one merge folds in 32
+    batches of 8.  At n = 131072 a single token moves LSE by 7.6e-6, under
+    the 1e-5 bound, so this pins the count to within a token (and any lost
+    or doubled piece by far)."""
+    b = W.make_batch(32, 8, starts=[131071, 5], qlens=[1, 1], seed=128, extra_pages=1)
+    counts = feattn.describe(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), b.blocks, b.qo, b.kv,
+                             b.pages, b.last, b.batch, b.rows)
+    assert counts[3] >= 128  # the long row is cut into that many partial rows at least
+    run_case(dev, b, True, "f16")
