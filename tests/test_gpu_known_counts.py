@@ -168,3 +168,12 @@ def test_counts_single_128k_sequence(dev):
                              b.pages, b.last, b.batch, b.rows)
     assert counts[3] >= 128  # the long row is cut into that many partial rows at least
     run_case(dev, b, True, "f16")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_exact_counts_long_chunks(dev, causal):
+    """An 8192-row chunk from an empty cache (row i sees exactly i + 1 keys
+    when causal) beside a 2048-row chunk over a 3000-token prefix: diagonal
+    tiles, splits and merges across many tile items."""
+    b = W.make_batch(32, 8, starts=[0, 3000], qlens=[8192, 2048], seed=81, extra_pages=1)
+    run_case(dev, b, causal, "f16")
