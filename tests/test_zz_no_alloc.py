@@ -71,3 +71,32 @@ def test_noalloc_rejects_calls_beyond_its_scratch(dev):
     assert b"scratch" in lib.fe_attn_last_error()
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
+
+
+def test_noalloc_rejects_bad_arguments(dev):
+    """The plan entry points' checks hold without a plan: head size,
+    alignment, negative batch and invalid metadata are refused on the host
+    with FE_EINVAL before any launch."""
+    b = W.make_batch(32, 8, starts=[100, 40], qlens=[1, 3], seed=9)
+    q = torch.zeros(b.rows, 32, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(b.blocks + 1, 16, 8, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.full_like(q, float("nan"))
+
+    def call(**kw):
+        args = dict(q=q, k_cache=kc, v_cache=kc, out=out, qo=b.qo, kv=b.kv, pages=b.pages, last=b.last,
+                    batch=b.batch, rows=b.rows, hq=32, hkv=8, dim=128, page=16, blocks=b.blocks, bf16=True)
+        args.update(kw)
+        return feattn.run_noalloc(**args)
+
+    with pytest.raises(RuntimeError, match="error -1"):
+        call(dim=64)
+    with pytest.raises(RuntimeError, match="error -1"):
+        call(q=q.view(-1)[4:].view(-1)[: q.numel() - 8])  # 8 bytes past the allocation start
+    with pytest.raises(RuntimeError, match="error -1"):
+        call(batch=-1)
+    bad_last = list(b.last)
+    bad_last[0] = 17
+    with pytest.raises(RuntimeError, match="error -1"):
+        call(last=bad_last)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
