@@ -91,78 +91,6 @@ __device__ __forceinline__ ShareStart ldc_share(const ShareStart* shares, int i)
   return r;
 }
 
-__device__ __forceinline__ DecodeMerge ldc_dmerge(const DecodeMerge* recs, int i) {
-  const int32_t* p = reinterpret_cast<const int32_t*>(recs + uniform(i));
-  return DecodeMerge{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3)};
-}
-
-// Merges the `dm.nsplit` partial rows of every (query row, head) of a
-// decode sequence (rows q0 .. q0+nq-1) into `out` / `lse`: the workgroup's
-// wavefronts take four (row, head) units at a time, 16 lanes per unit and 8
-// dims per lane.  Same arithmetic as attn_merge_kernel (batches of
-// kMergeBatch splits folded against a running maximum).
-constexpr int kMergeBatch = 8;
-
-template <bool BF16, int WAVES>
-__device__ __forceinline__ void decode_merge_rows(const AttnArgs& a, const DecodeMerge& dm, int q0, int nq, int wave,
-                                                  int lane) {
-  const int hq = a.hq;
-  const int units = nq * hq;
-  const int d = 8 * (lane & 15);
-  for (int u0 = 4 * wave; u0 < units; u0 += 4 * WAVES) {
-    const int u = u0 + (lane >> 4);
-    const bool on = u < units;
-    const int uu = on ? u : units - 1;
-    const int r = uu / hq;
-    const int h = uu - r * hq;
-    float m = kNegInf, wsum = 0.f;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int sp0 = 0; sp0 < dm.nsplit; sp0 += kMergeBatch) {
-      float l[kMergeBatch];
-      u32x4 rv[kMergeBatch];  // eight 16-bit partial values
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) {
-        l[b] = kNegInf;
-        rv[b] = u32x4{0u, 0u, 0u, 0u};
-        if (sp0 + b < dm.nsplit) {  // wave-uniform
-          const size_t slot = (size_t)(dm.part + (sp0 + b) * nq + r);
-          l[b] = a.part_lse[slot * hq + h];
-          rv[b] = *reinterpret_cast<const u32x4*>(a.part_o + (slot * hq + h) * kHeadDim + d);
-        }
-      }
-      float bm = m;
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) bm = fmaxf(bm, l[b]);
-      const float mu = bm == kNegInf ? 0.f : bm;
-      const float sc = fast_exp2(m - mu);
-      wsum *= sc;
-      acc0 *= sc;
-      acc1 *= sc;
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; ++b) {
-        const float wt = fast_exp2(l[b] - mu);
-        wsum += wt;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          acc0[2 * e] = __builtin_fmaf(wt, lo_f32<BF16>(rv[b][e]), acc0[2 * e]);
-          acc0[2 * e + 1] = __builtin_fmaf(wt, hi_f32<BF16>(rv[b][e]), acc0[2 * e + 1]);
-          acc1[2 * e] = __builtin_fmaf(wt, lo_f32<BF16>(rv[b][2 + e]), acc1[2 * e]);
-          acc1[2 * e + 1] = __builtin_fmaf(wt, hi_f32<BF16>(rv[b][2 + e]), acc1[2 * e + 1]);
-        }
-      }
-      m = bm;
-    }
-    if (on) {
-      const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-      const size_t oi = (size_t)(q0 + r) * hq + h;
-      const u32x4 o = {pack2<BF16>(acc0[0] * inv, acc0[1] * inv), pack2<BF16>(acc0[2] * inv, acc0[3] * inv),
-                       pack2<BF16>(acc1[0] * inv, acc1[1] * inv), pack2<BF16>(acc1[2] * inv, acc1[3] * inv)};
-      *reinterpret_cast<u32x4*>(a.out + oi * kHeadDim + d) = o;
-      if (a.lse != nullptr && (lane & 15) == 0) a.lse[oi] = wsum > 0.f ? (m + __log2f(wsum)) * kLn2 : kNegInf;
-    }
-  }
-}
-
 // NCB: 16-column blocks per item (1 or 2: up to 32 (query row, head)
 // columns, e.g. 8 verify rows with 4 heads per kv head).  Four blocks would
 // need more than the 256 registers of two wavefronts per SIMD.
@@ -180,17 +108,11 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
   const int pmask = (1 << pshift) - 1;
   const uint32_t ring = (uint32_t)(uintptr_t)dsm + (uint32_t)(wave * U * kDecUnit);
 
-  // Workgroup -> planner workgroup w: the launch places workgroup b on XCD
-  // b % 8, and w = (b % 8) * per + b / 8 puts consecutive planner workgroups
-  // (consecutive shares: the pieces of one sequence) on one XCD.
   // Wavefront slot -> (kv head, share): consecutive slots are consecutive
   // kv heads of one share (WAVES divides hkv, so a workgroup holds one
   // share and its wavefronts walk the same blocks).  Records past the
   // shares in use are empty.
-  const int per = uniform(ldc(a.dper, 0));
-  const int bgrp = blockIdx.x / kXcds;
-  if (bgrp >= per) return;
-  const int slot = ((blockIdx.x % kXcds) * per + bgrp) * WAVES + wave;
+  const int slot = blockIdx.x * WAVES + wave;
   const int kvh = slot % a.hkv;
   const int share = slot / a.hkv;
   if (share >= a.n_share_cap) return;
@@ -468,57 +390,6 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       }
     }
   }
-
-  // ---- split sequences: the share's first and last pieces may be pieces of
-  // sequences cut over several shares.  The workgroup counts itself off on
-  // each such sequence once its partials are stored; the last workgroup to
-  // arrive merges the sequence (every head and row).
-  if (a.dmerge == nullptr) return;
-  const DecodeItem wl = it_end - 1 > it_begin ? ldc_ditem(a.ditems, it_end - 1) : rec.first;
-  DecodeMerge dm0{}, dm1{};
-  if (rec.first.part >= 0) dm0 = ldc_dmerge(a.dmerge, rec.first.seq);
-  if (it_end - 1 > it_begin && wl.part >= 0) dm1 = ldc_dmerge(a.dmerge, wl.seq);
-  if (dm0.wgs == 0 && dm1.wgs == 0) return;
-  // This wavefront's partial stores have reached the L2, then every
-  // wavefront's (the ring is idle from here on: its first bytes hold the
-  // arrival results).
-  wait_vmem<0>();
-  lds_barrier();
-  int32_t* arrival = reinterpret_cast<int32_t*>(dsm);
-  if (wave == 0) {
-    const bool cross = ((dm0.wgs > 0) & dm0.flags) | ((dm1.wgs > 0) & dm1.flags);
-    // Pieces on other XCDs: write this L2 back before counting off.
-    if (cross) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    int last0 = 0, last1 = 0;
-    if (lane == 0) {
-      if (dm0.wgs > 0)
-        last0 = __hip_atomic_fetch_add(a.dcnt + rec.first.seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                dm0.wgs - 1;
-      if (dm1.wgs > 0)
-        last1 = __hip_atomic_fetch_add(a.dcnt + wl.seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == dm1.wgs - 1;
-    }
-    last0 = __builtin_amdgcn_readlane(last0, 0);
-    last1 = __builtin_amdgcn_readlane(last1, 0);
-    if (last0 | last1) {
-      // Partials from other XCDs: device-scope acquire (L1 and L2
-      // invalidated); from this XCD: they are in this L2, so only this
-      // compute unit's L1 is invalidated.
-      if ((last0 & dm0.flags) | (last1 & dm1.flags)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      else l1_invalidate();
-      // every workgroup of these sequences has arrived: reset for the next launch
-      if (lane == 0) {
-        if (last0) __hip_atomic_store(a.dcnt + rec.first.seq, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (last1) __hip_atomic_store(a.dcnt + wl.seq, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    if (lane == 0) {
-      arrival[0] = last0;
-      arrival[1] = last1;
-    }
-  }
-  lds_barrier();
-  if (uniform(arrival[0])) decode_merge_rows<BF16, WAVES>(a, dm0, rec.first.q0, rec.first.nq, wave, lane);
-  if (uniform(arrival[1])) decode_merge_rows<BF16, WAVES>(a, dm1, wl.q0, wl.nq, wave, lane);
 }
 
 // ===========================================================================
@@ -860,6 +731,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     const int h = 2 * (pair % hpairs) + (lane >> 5);
     const bool on = h < hq;
     const int hh = on ? h : hq - 1;
+    constexpr int kMergeBatch = 8;
     float m = kNegInf, wsum = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = 0; sp0 < mr.nsplit; sp0 += kMergeBatch) {
@@ -885,11 +757,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         const float wt = fast_exp2(l[u] - mu);
+        const f32x4 v = {lo_f32<BF16>(rv[u][0]), hi_f32<BF16>(rv[u][0]), lo_f32<BF16>(rv[u][1]),
+                         hi_f32<BF16>(rv[u][1])};
         wsum += wt;
-        acc[0] = __builtin_fmaf(wt, lo_f32<BF16>(rv[u][0]), acc[0]);
-        acc[1] = __builtin_fmaf(wt, hi_f32<BF16>(rv[u][0]), acc[1]);
-        acc[2] = __builtin_fmaf(wt, lo_f32<BF16>(rv[u][1]), acc[2]);
-        acc[3] = __builtin_fmaf(wt, hi_f32<BF16>(rv[u][1]), acc[3]);
+        acc += wt * v;
       }
       m = bm;
     }
@@ -904,25 +775,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
 }
 
 // ===========================================================================
-// XCD placement probe
-// ===========================================================================
-// Records the XCD each workgroup runs on (the XCC_ID hardware register), so
-// the host can check that workgroups b and b % 8 of a launch share an XCD,
-// and with it an L2.
-__global__ __launch_bounds__(64) void xcd_probe_kernel(uint8_t* out) {
-  uint32_t xcc;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-  if (threadIdx.x == 0) out[blockIdx.x] = (uint8_t)(xcc & 0xff);
-}
-
-hipError_t launch_xcd_probe(uint8_t* out, int grid, hipStream_t st) {
-  hipLaunchKernelGGL(xcd_probe_kernel, dim3(grid), dim3(64), 0, st, out);
-  return hipGetLastError();
-}
-
-// ===========================================================================
 // Launchers
 // ===========================================================================
+// Wavefronts per decode workgroup: consecutive kv heads of one share, as
+// many as divide hkv (at most kDecodeWavesPerCu).
+int decode_wg_waves(int hkv) {
+  for (int w = kDecodeWavesPerCu; w > 1; w >>= 1)
+    if (hkv % w == 0) return w;
+  return 1;
+}
+
 template <bool BF16, int WAVES, int NCB>
 static hipError_t decode_launch(const AttnArgs& a, int causal, int grid, hipStream_t st) {
   const size_t lds = (size_t)WAVES * dec_units<WAVES>() * kDecUnit + 16;

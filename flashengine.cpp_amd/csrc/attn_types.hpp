@@ -15,15 +15,6 @@ constexpr int kTileTokens = 64;  // tokens per KV tile of the MFMA tile kernel (
 constexpr int kTileCols = 128;   // (q row, head) columns per tile work item (4 waves x 32)
 constexpr int kDecodeCols = 32;  // max (q row, head) columns of one decode work item (2 MFMA N blocks)
 constexpr int kDecodeWavesPerCu = 8;  // decode wavefronts resident per CU (one kv head each)
-constexpr int kXcds = 8;  // XCDs of an MI355X; a launch places workgroup b on XCD b % 8
-
-// Wavefronts per decode workgroup: consecutive kv heads of one share, as
-// many as divide hkv (at most kDecodeWavesPerCu).
-inline int decode_wg_waves(int hkv) {
-  for (int w = kDecodeWavesPerCu; w > 1; w >>= 1)
-    if (hkv % w == 0) return w;
-  return 1;
-}
 
 // Per sequence, derived from the CSR metadata exactly as the reference ATen
 // plan does (portable_gpu_ops.cpp:30): len = (kv[b+1]-kv[b]-1)*page + last[b].
@@ -81,20 +72,6 @@ struct alignas(64) ShareStart {
 static_assert(sizeof(ShareStart) == 64, "one 64-byte scalar load");
 static_assert(sizeof(DecodeItem) == 32, "two pieces per 64 bytes");
 
-// Merge record of a decode sequence cut into `nsplit` pieces (partial slot
-// of piece p, row r: part + p*nq + r).  The decode kernel's workgroups that
-// hold its pieces (`wgs` of them) count themselves off on the sequence's
-// counter after writing their partials; the last one merges.  Bit 0 of
-// `flags`: the pieces span more than one XCD, so the partials are published
-// and read with device-scope release / acquire instead of through the one
-// L2 the workgroups share.  wgs == 0: merged by the merge kernel instead.
-struct DecodeMerge {
-  int32_t part;
-  int32_t nsplit;
-  int32_t wgs;
-  int32_t flags;
-};
-
 // One query row whose tokens were split over `nsplit` work items.  Split s
 // of this row lives in partial slot part + s*stride.
 struct MergeRow {
@@ -119,9 +96,6 @@ struct AttnArgs {
   const DecodeItem* ditems;  // decode only: the pieces, share by share
   const ShareStart* shares;  // decode only: one record per share
   int n_share_cap;           // decode only: records in `shares`
-  const DecodeMerge* dmerge; // decode only: per sequence (null: every merge by the merge kernel)
-  int32_t* dcnt;             // decode only: per-sequence arrival counters, zero between launches
-  const int32_t* dper;       // decode only: workgroups per XCD group (device-resident)
   uint16_t* part_o;        // [slots][hq][128] in the attention's 16-bit type, normalised per split
   float* part_lse;         // [slots][hq] log2 domain
   int hq;

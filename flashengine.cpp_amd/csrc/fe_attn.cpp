@@ -15,8 +15,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <atomic>
-#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -26,8 +24,8 @@
 
 namespace feattn {
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st);
+int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
-hipError_t launch_xcd_probe(uint8_t* out, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
                        bool bf16, int max_pos, hipStream_t st);
@@ -86,7 +84,7 @@ struct Regions {
 // Offsets of the regions inside a metadata arena (same layout on host and device).
 struct Layout {
   Regions n;
-  size_t seqs, pages, counts, dshare, decode, dmerge, dcnt, tile[2], tshare[2], merge[2], total;
+  size_t seqs, pages, counts, dshare, decode, tile[2], tshare[2], merge[2], total;
 };
 
 Layout make_layout(const Regions& r) {
@@ -103,11 +101,6 @@ Layout make_layout(const Regions& r) {
   off = align256(off + sizeof(ShareStart) * r.shares);
   l.decode = off;
   off = align256(off + sizeof(DecodeItem) * r.decode);
-  // decode merge records and arrival counters: one per sequence
-  l.dmerge = off;
-  off = align256(off + sizeof(DecodeMerge) * r.seqs);
-  l.dcnt = off;
-  off = align256(off + sizeof(int32_t) * r.seqs);
   for (int m = 0; m < 2; ++m) {
     l.tile[m] = off;
     off = align256(off + sizeof(WorkItem) * r.tile[m]);
@@ -137,39 +130,7 @@ Regions capacity_regions(const PlanShape& sh) {
 }
 
 // counts[] indices
-enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4, kCntDecodePer = 5 };
-
-// Whether the decode kernel may merge split sequences itself: workgroups b
-// and b % 8 of a launch must run on one XCD (the round-robin placement of
-// workgroups over the XCDs that its share grouping relies on).  Checked once
-// per device with a probe launch of 1024 workgroups on `st`, which writes
-// 1024 bytes at `dev_buf`.  The environment variable FEATTN_MERGE_KERNEL=1
-// sends every split through the merge kernel instead.
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_xcd_groups[kMaxDevices];  // 0 unknown, 1 shared XCDs, 2 not
-
-int decide_inline_merge(int device, uint8_t* dev_buf, hipStream_t st, bool& inline_merge) {
-  inline_merge = false;
-  const char* force = std::getenv("FEATTN_MERGE_KERNEL");
-  if (force != nullptr && force[0] != '\0' && std::strcmp(force, "0") != 0) return FE_OK;
-  if (device < 0 || device >= kMaxDevices) return FE_OK;
-  int v = g_xcd_groups[device].load(std::memory_order_acquire);
-  if (v == 0) {
-    constexpr int kProbe = 1024;
-    hipError_t e = launch_xcd_probe(dev_buf, kProbe, st);
-    if (e != hipSuccess) return hip_fail(e, "XCD probe launch");
-    std::vector<uint8_t> seen(kProbe);
-    e = hipMemcpyAsync(seen.data(), dev_buf, kProbe, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipStreamSynchronize(st);
-    if (e != hipSuccess) return hip_fail(e, "XCD probe readback");
-    bool same = true;
-    for (int b = kXcds; b < kProbe; ++b) same = same && seen[b] == seen[b % kXcds];
-    v = same ? 1 : 2;
-    g_xcd_groups[device].store(v, std::memory_order_release);
-  }
-  inline_merge = v == 1;
-  return FE_OK;
-}
+enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
 
 // Validated shape (host-only sizes).
 int make_shape(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks, PlanShape& sh,
@@ -195,9 +156,7 @@ int device_sizes(PlanShape& sh, int device, std::string& err) {
     return FE_EDEVICE;
   }
   sh.num_cus = cus > 0 ? cus : 256;
-  // a multiple of 64 wavefronts, so that the decode grid (decode_waves /
-  // wavefronts per workgroup) splits into equal XCD groups
-  sh.decode_waves = std::max(64, sh.num_cus * kDecodeWavesPerCu / 64 * 64);
+  sh.decode_waves = sh.num_cus * kDecodeWavesPerCu;
   sh.tile_slots = sh.num_cus * 2;  // 2 resident 256-thread tile workgroups per CU
   return FE_OK;
 }
@@ -216,10 +175,6 @@ int write_image(uint8_t* h, const Layout& l, const PlanShape& sh, const BuiltPla
   int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
   std::memset(cnt, 0, sizeof(int32_t) * 8);
   cnt[kCntDecode] = n_shares;
-  cnt[kCntDecodePer] = bp.decode_per;
-  // merge records of the call's sequences; the counters start at zero
-  if (!bp.dmerge.empty()) std::memcpy(h + l.dmerge, bp.dmerge.data(), sizeof(DecodeMerge) * bp.dmerge.size());
-  std::memset(h + l.dcnt, 0, sizeof(int32_t) * bp.seqs.size());
   // Every record up to the capacity is written: a graph launch covers them
   // all, and records past the shares in use must read as empty.
   std::memcpy(h + l.dshare, bp.decode_starts.data(), sizeof(ShareStart) * n_shares);
@@ -260,7 +215,6 @@ struct Launch {
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;         // wavefronts per decode workgroup
   int decode_nc = 16;
-  int decode_per = 1;        // decode workgroups per XCD group
   int grid_decode_cap = 0, grid_tile_cap = 0, grid_merge_cap = 0;
 };
 
@@ -277,7 +231,6 @@ void init_launch(Launch& L, const PlanShape& sh, bool bf16) {
 void record_lists(Launch& L, const BuiltPlan& bp, int nc) {
   L.decode_nc = nc;
   L.n_decode = (int)bp.decode_starts.size() * L.sh.hkv;  // busy decode wavefronts
-  L.decode_per = bp.decode_per;
   for (int m = 0; m < 2; ++m) {
     L.n_tile[m] = (int)bp.mode[m].tile.size();
     L.n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
@@ -326,12 +279,8 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
     d.shares = reinterpret_cast<const ShareStart*>(L.dev + L.lay.dshare);
     d.n_share_cap = (int)L.lay.n.shares;
     d.n_items = counts + kCntDecode;
-    d.dmerge = L.sh.inline_merge ? reinterpret_cast<const DecodeMerge*>(L.dev + L.lay.dmerge) : nullptr;
-    d.dcnt = reinterpret_cast<int32_t*>(const_cast<uint8_t*>(L.dev) + L.lay.dcnt);
-    d.dper = counts + kCntDecodePer;
-    // eager: the XCD groups of the shares in use (kXcds * decode_per
-    // workgroups); graph: the capacity grid, a multiple of kXcds
-    const int grid = L.graph ? L.grid_decode_cap : std::min(L.grid_decode_cap, kXcds * L.decode_per);
+    const int wv = L.decode_wg;
+    const int grid = L.graph ? L.grid_decode_cap : std::min(L.grid_decode_cap, (L.n_decode + wv - 1) / wv);
     e = launch_decode(d, L.bf16, L.decode_wg, L.decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
   }
@@ -395,10 +344,6 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   if (rc != FE_OK) return fail(rc, err);
   rc = check_tensors(q, k_cache, v_cache, out, lse);
   if (rc != FE_OK) return rc;
-  // (the probe, on the first call on a device, writes the arena's first
-  // bytes before the metadata copy below does)
-  rc = decide_inline_merge(device, arena, st, sh.inline_merge);
-  if (rc != FE_OK) return rc;
   BuiltPlan bp;
   rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
@@ -422,10 +367,10 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   if (need > bytes)
     return fail(FE_ECAPACITY, "attention (no-alloc): this call needs " + std::to_string(need) +
                                   " bytes of device scratch, more than the " + std::to_string(bytes) + " it holds");
-  // Nothing else in the arena has to start at zero, whatever an earlier call
+  // Nothing in the arena has to start at zero, whatever an earlier call
   // left there: the copy below writes every metadata field the kernels read
-  // (counts, share records, lists, zeroed merge counters), and every partial
-  // slot a merge reads is written by this call's decode or tile kernel first.
+  // (counts, share records, lists), and every partial slot a merge reads is
+  // written by this call's decode or tile kernel first.
   std::vector<uint8_t> image(L.lay.total);
   rc = write_image(image.data(), L.lay, sh, bp, pages, npages, err);
   if (rc != FE_OK) return fail(rc, err);
@@ -495,11 +440,6 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
     return cleanup(FE_ENOMEM, "hipMalloc(split-KV lse) failed");
   if (hipEventCreateWithFlags(&p->staged, hipEventDisableTiming) != hipSuccess)
     return cleanup(FE_EDEVICE, "hipEventCreate failed");
-  // (the probe writes the arena's first bytes; the memset below clears them)
-  bool inline_merge = false;
-  rc = decide_inline_merge(dev, p->dev, nullptr, inline_merge);
-  if (rc != FE_OK) return cleanup(rc, g_error);
-  p->run.sh.inline_merge = inline_merge;
   // Counts start at zero so a run before any prepare does nothing.
   if (hipMemset(p->dev, 0, total) != hipSuccess) return cleanup(FE_EDEVICE, "hipMemset(plan) failed");
   if (hipDeviceSynchronize() != hipSuccess) return cleanup(FE_EDEVICE, "hipDeviceSynchronize failed");
@@ -571,8 +511,6 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
   if (e == hipSuccess) e = copy(l.dshare, sizeof(ShareStart) * l.n.shares);
   if (e == hipSuccess) e = copy(l.decode, sizeof(DecodeItem) * bp.decode_items.size());
-  if (e == hipSuccess) e = copy(l.dmerge, sizeof(DecodeMerge) * bp.dmerge.size());
-  if (e == hipSuccess) e = copy(l.dcnt, sizeof(int32_t) * bp.seqs.size());
   for (int m = 0; m < 2 && e == hipSuccess; ++m) {
     e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
     if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * l.n.tshare[m]);
@@ -715,48 +653,11 @@ int fe_attn_plan_describe(int hq, int hkv, int dim, int page, int max_batch, int
   const int rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   if (counts_out) {
-    // merged rows: the merge kernel's plus those of the decode sequences
-    // that the decode kernel merges itself
-    int32_t merged = (int32_t)bp.mode[1].merge.size();
-    for (size_t b = 0; b < bp.dmerge.size(); ++b)
-      if (bp.dmerge[b].wgs > 0) merged += bp.seqs[b].qlen;
     counts_out[0] = (int32_t)bp.decode.size() * hkv;
     counts_out[1] = (int32_t)bp.mode[1].tile.size();
-    counts_out[2] = merged;
+    counts_out[2] = (int32_t)bp.mode[1].merge.size();
     counts_out[3] = bp.mode[1].partial_rows;
   }
-  return FE_OK;
-}
-
-int fe_attn_plan_decode_merges(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks,
-                               const int32_t* qo, const int32_t* kv, const int32_t* pages, const int32_t* last,
-                               int batch, int rows, int32_t* recs_out, int32_t* groups_out) {
-  PlanShape sh;
-  std::string err;
-  int rc = make_shape(hq, hkv, dim, page, max_batch, max_pages, blocks, sh, err);
-  if (rc != FE_OK) return fail(rc, err);
-  BuiltPlan bp;
-  rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
-  if (rc != FE_OK) return fail(rc, err);
-  const int nshares = (int)bp.decode_starts.size();
-  for (int b = 0; b < batch; ++b) {
-    int32_t* o = recs_out + 6 * b;
-    const DecodeMerge dm = (size_t)b < bp.dmerge.size() ? bp.dmerge[b] : DecodeMerge{0, 0, 0, 0};
-    o[0] = dm.part;
-    o[1] = dm.nsplit;
-    o[2] = dm.wgs;
-    o[3] = dm.flags;
-    o[4] = -1;  // first and last share holding a piece of the sequence
-    o[5] = -1;
-  }
-  for (int k = 0; k < nshares; ++k)
-    for (int i = bp.decode_share_off[k]; i < bp.decode_share_off[k + 1]; ++i) {
-      int32_t* o = recs_out + 6 * bp.decode[i].seq;
-      if (o[4] < 0) o[4] = k;
-      o[5] = k;
-    }
-  groups_out[0] = bp.decode_per;
-  groups_out[1] = nshares;
   return FE_OK;
 }
 

@@ -75,14 +75,6 @@ __device__ __forceinline__ void wait_units(int n) {
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Workgroup barrier after this wavefront's LDS operations have completed; a
-// compiler barrier for memory accesses on both sides.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Invalidates this compute unit's vector L1, so that the loads after it read
-// what other compute units of the same XCD stored into the shared L2.
-__device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <bool BF16>

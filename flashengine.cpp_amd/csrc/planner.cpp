@@ -237,13 +237,6 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
     }
     const int used = (int)cuts.size() - 1;
     out.decode_share_off.assign(used + 1, 0);
-    // Workgroups: share k is held by workgroups k*wgs_share .. +wgs_share-1
-    // (one wavefront per kv head), and the decode kernel runs workgroup w on
-    // XCD w / decode_per, so that consecutive shares -- the pieces of one
-    // sequence -- share an L2.
-    const int wgs_share = sh.hkv / decode_wg_waves(sh.hkv);
-    out.decode_per = std::max(1, ceil_div(used * wgs_share, kXcds));
-    out.dmerge.assign((size_t)batch, DecodeMerge{0, 0, 0, 0});
     int64_t off = 0;
     int share = 0;
     size_t k = 0;
@@ -259,13 +252,7 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
       if (np > 1) {
         base = out.decode_partials;
         out.decode_partials += np * s.qlen;
-        if (sh.inline_merge) {
-          const int w0 = (int)k * wgs_share, w1 = (int)(k1 + 1) * wgs_share - 1;
-          const bool cross = w0 / out.decode_per != w1 / out.decode_per;
-          out.dmerge[b] = DecodeMerge{base, np, np * wgs_share, cross ? 1 : 0};
-        } else {
-          for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, np, s.qlen});
-        }
+        for (int r = 0; r < s.qlen; ++r) out.decode_merge.push_back(MergeRow{s.qo + r, base + r, np, s.qlen});
       }
       for (size_t j = k; j <= k1; ++j) {
         while (share < (int)j) out.decode_share_off[++share] = (int32_t)out.decode.size();

@@ -24,7 +24,6 @@ struct PlanShape {
   int tile_slots = 512;     // workgroups of one tile launch (two resident per CU)
   int item_cap = 1 << 16;   // work items per list
   int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
-  bool inline_merge = true; // decode splits merged by the decode kernel's last workgroup
 };
 
 struct ModeLists {
@@ -41,9 +40,7 @@ struct BuiltPlan {
   std::vector<DecodeItem> decode_items;   // `decode` in the decode kernel's format
   std::vector<ShareStart> decode_starts;  // one per share in use
   int decode_partials = 0;
-  std::vector<MergeRow> decode_merge;    // merge-kernel rows of split decode sequences (!inline_merge)
-  std::vector<DecodeMerge> dmerge;       // per sequence (inline_merge; zero for unsplit ones)
-  int decode_per = 1;                    // decode workgroups per XCD group (ceil(workgroups / 8))
+  std::vector<MergeRow> decode_merge;
   int decode_nc = 16;            // 16 or 32 columns per decode item (MFMA column blocks x 16)
   ModeLists mode[2];             // [0] full (non-causal), [1] causal
 };

@@ -41,7 +41,6 @@ C_SYMBOLS = (
     "fe_attn_version",
     "fe_attn_run_noalloc",
     "fe_attn_assign_shares",
-    "fe_attn_plan_decode_merges",
 )
 
 # Every extern "C" symbol of include/fe_driver.h.
@@ -99,7 +98,6 @@ def lib() -> ctypes.CDLL:
     L.fe_store.argtypes = [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _int]
     L.fe_rope_append.argtypes = [_vp] * 8 + [_int] * 7 + [_vp]
     L.fe_attn_plan_describe.argtypes = [_int] * 7 + [_i32p] * 4 + [_int, _int, _i32p]
-    L.fe_attn_plan_decode_merges.argtypes = [_int] * 7 + [_i32p] * 4 + [_int, _int, _i32p, _i32p]
     L.fe_attn_plan_dump.argtypes = [_int] * 7 + [_i32p] * 4 + [_int, _int, _int, _i32p, _int,
                                                              ctypes.POINTER(_int)]
     for name in C_SYMBOLS:
@@ -234,17 +232,6 @@ def describe(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, la
     _check(lib().fe_attn_plan_describe(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
                                        _i32(kv), _i32(pages), _i32(last), batch, rows, out))
     return tuple(out)
-
-
-def decode_merges(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, last, batch, rows):
-    """Host-only planner dump of the decode merges: (records, groups) with one
-    record (part, nsplit, wgs, cross, first_share, last_share) per sequence and
-    groups = (decode workgroups per XCD group, decode shares)."""
-    recs = (ctypes.c_int32 * (6 * max(1, batch)))()
-    groups = (ctypes.c_int32 * 2)()
-    _check(lib().fe_attn_plan_decode_merges(hq, hkv, dim, page, max_batch, max_pages, blocks, _i32(qo),
-                                            _i32(kv), _i32(pages), _i32(last), batch, rows, recs, groups))
-    return [tuple(recs[6 * b:6 * b + 6]) for b in range(batch)], tuple(groups)
 
 
 def assign_shares(costs: Sequence[int], slots: int):

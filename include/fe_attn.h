@@ -163,21 +163,6 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch,
                       const int32_t* last, int batch, int rows, int causal,
                       int32_t* items_out, int cap, int* n_out);
 
-/* Host-only planner dump of the decode merges (no device needed; a 256-CU
- * device assumed, as fe_attn_plan_describe does): per sequence b, six int32
- * at recs_out[6b]: first partial slot, pieces, decode workgroups that hold
- * them (0: not split), cross-XCD flag (1: the pieces' workgroups are in
- * more than one XCD group), first and last share holding a piece (-1: no
- * decode piece).  groups_out[0] = workgroups per XCD group (the decode
- * kernel runs planner workgroup w on XCD w / groups_out[0]), groups_out[1] =
- * decode shares.  For tests of the decode kernel's in-kernel merge. */
-int fe_attn_plan_decode_merges(int hq, int hkv, int dim, int page,
-                               int max_batch, int max_pages, int blocks,
-                               const int32_t* qo, const int32_t* kv,
-                               const int32_t* pages, const int32_t* last,
-                               int batch, int rows, int32_t* recs_out,
-                               int32_t* groups_out);
-
 /* Host-only: the share assignment fe_attn_plan_prepare gives tile items
  * (one share per tile workgroup), on caller-chosen costs, for tests.  Longest
  * processing time: items in decreasing cost order (equal costs keep their

@@ -179,69 +179,3 @@ def test_share_assignment_rejects_bad_input():
         feattn.assign_shares([3, -1], 4)
     with pytest.raises(RuntimeError, match="slots"):
         feattn.assign_shares([3], 0)
-
-
-def waves_per_wg(hkv):
-    w = 8
-    while w > 1 and hkv % w:
-        w //= 2
-    return w
-
-
-@pytest.mark.parametrize("case", ["headline", "long", "mixed30b", "hkv16", "hkv6", "hkv1", "tiny"])
-def test_decode_merge_records(case):
-    """The decode kernel merges a split sequence in the last of its pieces'
-    workgroups: each record must count those workgroups exactly, and the
-    cross-XCD flag must be set exactly when they fall in more than one XCD
-    group (planner workgroup w runs on XCD w // per; share k is held by
-    workgroups k*m .. k*m+m-1, m = hkv / wavefronts per workgroup)."""
-    if case == "headline":
-        b = W.qwen3_8b_decode()
-    elif case == "long":
-        b = W.long_decode(batch=16)
-    elif case == "mixed30b":
-        b = W.qwen3_30b_mixed()
-    elif case == "hkv16":
-        b = W.make_batch(64, 16, starts=[3000, 700, 9000, 1], qlens=[1, 2, 1, 1], seed=9)
-    elif case == "hkv6":
-        b = W.make_batch(24, 6, starts=list(range(100, 6100, 300)), qlens=[1] * 20, seed=10)
-    elif case == "hkv1":
-        b = W.make_batch(8, 1, starts=[5000, 20, 12000], qlens=[1, 4, 1], seed=11)
-    else:
-        b = W.make_batch(32, 8, starts=[40, 3], qlens=[1, 5], seed=1)
-    recs, (per, nshares) = feattn.decode_merges(*plan_args(b))
-    m = b.hkv // waves_per_wg(b.hkv)
-    cap = 2048 // waves_per_wg(b.hkv)          # decode grid of a 256-CU device
-    assert per == max(1, -(-nshares * m // 8))
-    assert 8 * per <= cap
-    pieces = {}
-    for kind, seq, q0, nq, kvh, t0, t1, part in feattn.dump(*plan_args(b), causal=True):
-        if kind == 0 and kvh == 0:
-            pieces.setdefault(seq, []).append((t0, part))
-    n_split = n_cross = 0
-    slot = 0
-    for s in range(b.batch):
-        part, nsplit, wgs, cross, k0, k1 = recs[s]
-        got = sorted(pieces.get(s, []))
-        if not got:
-            assert (wgs, k0, k1) == (0, -1, -1)
-            continue
-        if len(got) == 1:
-            assert wgs == 0 and got[0][1] == -1
-            continue
-        n_split += 1
-        qlen = b.qlens[s]
-        assert nsplit == len(got) == k1 - k0 + 1
-        assert wgs == nsplit * m
-        assert [p for _, p in got] == [part + j * qlen for j in range(nsplit)]
-        assert part == slot  # decode partial slots are handed out in sequence order
-        slot += nsplit * qlen
-        want_cross = (k0 * m) // per != ((k1 + 1) * m - 1) // per
-        assert bool(cross) == want_cross
-        n_cross += cross
-    if case in ("headline", "long"):
-        assert n_split > 0
-        # contiguous XCD groups: only sequences across a group boundary are cross
-        assert n_cross <= 7
-    counts = feattn.describe(*plan_args(b))
-    assert counts[2] >= sum(b.qlens[s] for s in range(b.batch) if recs[s][2] > 0)
