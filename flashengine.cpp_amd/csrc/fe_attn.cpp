@@ -238,6 +238,19 @@ void record_lists(Launch& L, const BuiltPlan& bp, int nc) {
   }
 }
 
+// The work of a call runs on the device of its stream (the current device
+// for the null stream); a plan's memory lives on the device it was created
+// on, and the two must agree.
+int check_stream_device(hipStream_t st, int device) {
+  int dev = -1;
+  const hipError_t e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+  if (dev != device)
+    return fail(FE_EDEVICE, "attention: stream on device " + std::to_string(dev) + ", plan memory on device " +
+                                std::to_string(device));
+  return FE_OK;
+}
+
 int check_tensors(const void* q, const void* k_cache, const void* v_cache, const void* out, const float* lse) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
     return fail(FE_EINVAL, "null tensor pointer");
@@ -343,6 +356,8 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   if (rc == FE_OK) rc = device_sizes(sh, device, err);
   if (rc != FE_OK) return fail(rc, err);
   rc = check_tensors(q, k_cache, v_cache, out, lse);
+  if (rc != FE_OK) return rc;
+  rc = check_stream_device(st, device);
   if (rc != FE_OK) return rc;
   BuiltPlan bp;
   rc = build_plan(sh, qo, kv, pages, last, batch, rows, bp, err);
@@ -468,7 +483,9 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   Launch& L = p->run;
   BuiltPlan bp;
   std::string err;
-  const int rc = build_plan(L.sh, qo, kv, pages, last, batch, rows, bp, err);
+  int rc = check_stream_device(static_cast<hipStream_t>(stream), p->device);
+  if (rc != FE_OK) return rc;
+  rc = build_plan(L.sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   int nc = bp.decode_nc;
   int graph_nc = p->graph_nc, graph_tile = L.graph_tile;
@@ -534,7 +551,9 @@ int fe_attn_run(fe_attn_plan* p, const void* q, const void* k_cache, const void*
                 int causal, void* stream) {
   if (p == nullptr) return fail(FE_EINVAL, "plan is null");
   if (!p->prepared) return fail(FE_EINVAL, "attention called before prepare_plan");
-  const int rc = check_tensors(q, k_cache, v_cache, out, lse);
+  int rc = check_tensors(q, k_cache, v_cache, out, lse);
+  if (rc != FE_OK) return rc;
+  rc = check_stream_device(static_cast<hipStream_t>(stream), p->device);
   if (rc != FE_OK) return rc;
   return launch_all(p->run, q, k_cache, v_cache, out, lse, causal, static_cast<hipStream_t>(stream));
 }

@@ -69,7 +69,9 @@ int fe_attn_plan_destroy(fe_attn_plan* plan);
  * [0, blocks], last in [1, page]), builds the decode / tile / merge work
  * lists and copies them to the plan's device buffers on `stream`.
  * `graph` != 0 pins the launch grids to the plan capacity so that a graph
- * captured once replays correctly after later prepares. */
+ * captured once replays correctly after later prepares.  `stream` must be
+ * on the device that was current when the plan was created (FE_EDEVICE
+ * otherwise), here and in fe_attn_run. */
 int fe_attn_plan_prepare(fe_attn_plan* plan, const int32_t* qo,
                          const int32_t* kv, const int32_t* pages,
                          const int32_t* last, int batch, int rows, int graph,
