@@ -84,6 +84,7 @@ CASES = [
     (128, 8, [1000, 64, 2500], [2, 3, 1]),                   # GQA 16: 2 rows fill a decode item
     (64, 2, [1500, 40], [1, 2]),                             # GQA 32
     (128, 1, [800, 20], [1, 2]),                             # GQA 128: one row is a whole tile item
+    (32, 16, [1200, 3, 600], [1, 9, 70]),                    # hkv 16: a decode share spans two workgroups
 ]
 
 

@@ -121,12 +121,13 @@ def test_exact_counts_prefill_chunks_non_causal_and_causal(dev, causal):
 
 
 @pytest.mark.parametrize("hq,hkv", [(16, 2), (24, 6), (40, 8), (8, 8), (24, 8), (48, 8), (128, 8), (64, 2),
-                                    (128, 1)])
+                                    (128, 1), (32, 16), (64, 16), (32, 32)])
 def test_exact_counts_head_layouts(dev, hq, hkv):
     """Head layouts whose decode workgroups hold 2 or 1 wavefronts (hkv = 2,
-    6, 1), non-power-of-two groups (3, 5, 6) and groups of 16 to 128 query
-    heads per kv head (a row alone fills a decode or a tile item), decode
-    and chunk rows mixed."""
+    6, 1), decode shares held by two or four workgroups of 8 wavefronts
+    (hkv = 16, 32), non-power-of-two groups (3, 5, 6) and groups of 16 to
+    128 query heads per kv head (a row alone fills a decode or a tile item),
+    decode and chunk rows mixed."""
     b = W.make_batch(hq, hkv, starts=[4095, 0, 777, 5000, 31], qlens=[1, 1, 1, 2, 90], seed=hq + hkv,
                      extra_pages=1)
     run_case(dev, b, True, "f16")
