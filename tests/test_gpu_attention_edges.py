@@ -288,6 +288,32 @@ def test_misaligned_tensors_are_refused(dev):
     check(out.cpu(), lse.cpu(), want_out, want_lse)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_null_lse_gives_the_same_output(dev, causal):
+    """The reference's attention has no LSE output (its call passes none):
+    with lse = NULL every kernel (decode, tile, both merges) must write the
+    same output bits as with an LSE buffer.  The batch splits decode
+    sequences (long contexts) and tile items (a long chunk)."""
+    b = W.make_batch(32, 8, starts=[9000, 40, 6000, 0], qlens=[1, 1, 3, 600], seed=31, extra_pages=1)
+    q, kc, vc = W.make_tensors(b, seed=31)
+    counts = feattn.describe(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), b.blocks, b.qo, b.kv,
+                             b.pages, b.last, b.batch, b.rows)
+    assert counts[2] > 0  # some rows are merged from split partials
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    with_lse = torch.zeros_like(qd)
+    lse = torch.full((b.rows, b.hq), float("nan"), device=dev)
+    plan.run(qd, kd, vd, with_lse, causal=causal, lse=lse)
+    no_lse = torch.zeros_like(qd)
+    plan.run(qd, kd, vd, no_lse, causal=causal, lse=None)
+    torch.cuda.synchronize()
+    plan.close()
+    assert torch.equal(with_lse.view(torch.int16), no_lse.view(torch.int16))
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    check(no_lse.cpu(), lse.cpu(), want_out, want_lse)
+
+
 def test_two_plans_on_two_streams(dev):
     """Two plans (a decode batch and a prefill batch, different shapes) are
     prepared and run on two streams at once, three times in a row; both
