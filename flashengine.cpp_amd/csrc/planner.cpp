@@ -87,6 +87,119 @@ void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>
   items.swap(grouped);
 }
 
+namespace {
+
+// Tile work list by an equal cut of the tile stream: the query-row chunks of
+// the tile sequences (qr rows each, over their visible token ranges), in
+// batch order, are laid end to end and cut at tile boundaries into `slots /
+// hkv` shares of equal cost (tiles x 16-column blocks per wavefront).  Every
+// kv head uses the same cut, and share k of kv head h goes to workgroup
+// k * hkv + h, so the workgroups of one share read the same pages at the same
+// time.  A chunk cut into several pieces gets partial slots and merge rows
+// as in the longest-first list.  Returns false, leaving `ml` alone, when the
+// cut needs more partial slots or items than `slot_budget` / `item_cap`.
+bool cut_tile_stream(const std::vector<SeqInfo>& seqs, int G, int hkv, bool causal, int slots, int partial_base,
+                     int slot_budget, int item_cap, ModeLists& ml) {
+  const int qr = kTileCols / G;
+  const int n_shares = slots / hkv;
+  if (n_shares < 1) return false;
+  struct Chunk {
+    int seq, q0, nq, extent, tiles, c;
+  };
+  std::vector<Chunk> ch;
+  int64_t total = 0;
+  for (int b = 0; b < (int)seqs.size(); ++b) {
+    const SeqInfo& s = seqs[b];
+    if (s.qlen * G <= kDecodeCols) continue;
+    for (int i0 = 0; i0 < s.qlen; i0 += qr) {
+      const int nq = std::min(qr, s.qlen - i0);
+      const int extent = causal ? std::min(s.len, s.len - s.qlen + i0 + nq) : s.len;
+      const int tiles = ceil_div(extent, kTileTokens);
+      const int c = nq * G > kTileCols / 2 ? 2 : 1;
+      ch.push_back(Chunk{b, s.qo + i0, nq, extent, tiles, c});
+      total += (int64_t)tiles * c;
+    }
+  }
+  if (ch.empty()) return false;
+  const int64_t quota = (total + n_shares - 1) / n_shares;
+  // Pieces in stream order: (chunk, first tile, tiles, share); the last share
+  // takes whatever rounding leaves over.
+  struct Piece {
+    int chunk, tile0, ntiles, share;
+  };
+  std::vector<Piece> pcs;
+  std::vector<int> npc(ch.size(), 0);
+  int share = 0;
+  int64_t load = 0;
+  for (int i = 0; i < (int)ch.size(); ++i) {
+    int done = 0;
+    while (done < ch[i].tiles) {
+      int take = ch[i].tiles - done;
+      if (share < n_shares - 1) {
+        int64_t room = (quota - load) / ch[i].c;
+        if (room <= 0) {
+          if (load > 0) {
+            ++share;
+            load = 0;
+            continue;
+          }
+          room = 1;
+        }
+        take = (int)std::min<int64_t>(room, take);
+      }
+      pcs.push_back(Piece{i, done, take, share});
+      ++npc[i];
+      done += take;
+      load += (int64_t)take * ch[i].c;
+      if (share < n_shares - 1 && load >= quota) {
+        ++share;
+        load = 0;
+      }
+    }
+  }
+  if ((int64_t)pcs.size() * hkv > item_cap) return false;
+  std::vector<int> base(ch.size(), -1);
+  int64_t rows = partial_base;
+  for (size_t i = 0; i < ch.size(); ++i)
+    if (npc[i] > 1) {
+      base[i] = (int)rows;
+      rows += (int64_t)npc[i] * ch[i].nq;
+    }
+  if (rows > slot_budget) return false;
+
+  ModeLists out;
+  out.partial_rows = (int)rows;
+  for (size_t i = 0; i < ch.size(); ++i)
+    if (base[i] >= 0)
+      for (int r = 0; r < ch[i].nq; ++r) out.merge.push_back(MergeRow{ch[i].q0 + r, base[i] + r, npc[i], ch[i].nq});
+  // Piece p's index within its chunk (pieces of a chunk are consecutive).
+  std::vector<int> sp(pcs.size());
+  for (size_t p = 0; p < pcs.size(); ++p) sp[p] = (p > 0 && pcs[p - 1].chunk == pcs[p].chunk) ? sp[p - 1] + 1 : 0;
+  const int used = pcs.back().share + 1;
+  out.tile.reserve(pcs.size() * (size_t)hkv);
+  out.tile_off.assign((size_t)used * hkv + 1, 0);
+  size_t p0 = 0;
+  for (int k = 0; k < used; ++k) {
+    size_t p1 = p0;
+    while (p1 < pcs.size() && pcs[p1].share == k) ++p1;
+    for (int h = 0; h < hkv; ++h) {
+      for (size_t p = p0; p < p1; ++p) {
+        const Chunk& c = ch[pcs[p].chunk];
+        const int t0 = pcs[p].tile0 * kTileTokens;
+        const int t1 = std::min(c.extent, (pcs[p].tile0 + pcs[p].ntiles) * kTileTokens);
+        const int part = base[pcs[p].chunk] < 0 ? -1 : base[pcs[p].chunk] + sp[p] * c.nq;
+        out.tile.push_back(WorkItem{c.seq, c.q0, c.nq, h, t0, t1, part, pcs[p].ntiles * c.c});
+      }
+      out.tile_off[(size_t)k * hkv + h + 1] = (int32_t)out.tile.size();
+    }
+    p0 = p1;
+  }
+  ml = std::move(out);
+  return true;
+}
+
+}  // namespace
+
 int validate_shape(const PlanShape& sh, std::string& err) {
   if (sh.dim != kHeadDim) {
     err = "attention supports head_dim 128 only (got " + std::to_string(sh.dim) + ")";
@@ -342,6 +455,16 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
       want = std::max(1, want / 2);
     }
     assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
+    // When the longest-first list had to split chunks anyway, an equal cut
+    // of the tile stream balances the workgroups to within a tile, usually
+    // with fewer pieces; it replaces the list if it needs no more partial rows.
+    if (ml.partial_rows > out.decode_partials) {
+      ModeLists cut;
+      if (cut_tile_stream(out.seqs, G, sh.hkv, causal != 0, sh.tile_slots, out.decode_partials, slot_budget,
+                          sh.item_cap, cut) &&
+          cut.partial_rows <= ml.partial_rows)
+        ml = std::move(cut);
+    }
   }
   for (int causal = 0; causal < 2; ++causal) {
     std::vector<MergeRow>& m = out.mode[causal].merge;

@@ -66,6 +66,40 @@ def test_coverage_gqa_variants():
         coverage(b, True)
 
 
+def test_tile_stream_cut_balances_block_verify():
+    """Sixteen 16-row non-causal blocks over long contexts (DFlash verify):
+    the tile list is the equal cut of the tile stream -- workgroup k * hkv + h
+    takes share k of kv head h, every kv head is cut alike, and no share
+    holds more than ceil(total tiles per kv head / (512 / hkv)) tiles."""
+    ctx = np.random.default_rng(11).integers(2000, 8001, size=16).tolist()
+    b = W.make_batch(32, 8, starts=ctx, qlens=[16] * 16, seed=11, extra_pages=1)
+    items = [it for it in coverage(b, False) if it[0] == 1]
+    d, t, m, p = feattn.describe(*plan_args(b))
+    assert m == 16 * sum(1 for s in range(16) if len([it for it in items if it[1] == s and it[4] == 0]) > 1)
+    # runs of equal kv head in list order: h = 0..7, then the next share
+    runs = []
+    for it in items:
+        if runs and runs[-1][0] == it[4]:
+            runs[-1][1].append(it)
+        else:
+            runs.append((it[4], [it]))
+    assert [h for h, _ in runs] == list(range(8)) * (len(runs) // 8)
+    strip = lambda r: [(x[1], x[2], x[3], x[5], x[6], x[7]) for x in r]
+    loads = []
+    for k in range(0, len(runs), 8):
+        for h in range(1, 8):
+            assert strip(runs[k + h][1]) == strip(runs[k][1])
+        loads.append(sum((x[6] - x[5] + 63) // 64 for x in runs[k][1]))
+    # kv head 0's pieces, share after share, are the stream in order
+    stream = [x for k in range(0, len(runs), 8) for x in runs[k][1]]
+    for a, c in zip(stream, stream[1:]):
+        assert (c[1], c[5]) == ((a[1], a[6]) if a[6] < b.lens[a[1]] else (a[1] + 1, 0))
+    total = sum((l + 16 + 63) // 64 for l in ctx)
+    quota = -(-total // 64)
+    assert sum(loads) == total
+    assert len(loads) <= 64 and max(loads) <= quota
+
+
 def test_split_kv_produces_merges():
     b = W.long_decode(batch=4, ctx=32768)
     counts = feattn.describe(*plan_args(b))
