@@ -11,9 +11,10 @@ so the 256 MB Infinity Cache cannot hold the working set.
 value = algorithmic decode bytes per step (visible K/V rows + q in + o out +
 page ids) / measured time per step, in GB/s.  Secondary figures (chunked
 prefill TFLOP/s, fused RoPE+append GB/s, DFlash block, mixed step,
-long-context decode) are reported under "secondary".  The CPU baseline is the
-oracle's LibTorch-CPU restatement of the reference's ATen attention on the
-same decode batch.
+long-context decode) are reported under "secondary"; `--only pattern` prints
+the read throughput of the cache access patterns alone (lib/libfeprobe.so).
+The CPU baseline is the oracle's LibTorch-CPU restatement of the reference's
+ATen attention on the same decode batch.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -123,7 +124,7 @@ def decode_headline(steps, warmup, dev):
 
 def secondary(dev, only=None):
     """Other workload shapes: ms per call and throughput.  `only` selects one
-    of prefill / dflash / mixed / long / graph."""
+    of prefill / dflash / mixed / long / graph / pattern."""
     import torch
 
     import feattn
@@ -146,6 +147,9 @@ def secondary(dev, only=None):
         _long(dev, res)
     if want("graph"):
         _graph(dev, res)
+    if only == "pattern":  # reference figures, not part of the default run
+        res["read_patterns"] = read_patterns(dev)
+        log("read patterns", res["read_patterns"])
     return res
 
 
@@ -313,6 +317,54 @@ def copy_calibration(dev, mib=1024):
     return {"bytes_per_copy": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / ms / 1e6, 1)}
 
 
+def read_patterns(dev):
+    """Read throughput of the cache access patterns alone (lib/libfeprobe.so,
+    no attention arithmetic): 2 GiB of 32 KB pages (16 rows of 8 kv heads x
+    256 B) in seeded-permutation chains of 64 pages; one kv head's 256 B of
+    every row per work unit (as a tile workgroup reads the cache), whole 2 KB
+    rows (as a decode workgroup's wavefronts read it together), and the tile
+    kernel's copy stream (K and V pools of 1 GiB each, direct-to-LDS copies,
+    one 64-token tile in flight per workgroup) without its compute."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
+    lib = ctypes.CDLL(path)
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    lib.fe_probe_rows.argtypes = [vp, vp, i, i, i, i, vp, vp]
+    lib.fe_probe_tile_copy.argtypes = [vp, vp, vp, i, i, i, vp, vp]
+    pool_pages, chain = 32768, 64
+    g = torch.Generator().manual_seed(7)
+    perm2 = torch.randperm(2 * pool_pages, generator=g).to(torch.int32).to(dev)
+    perm1 = torch.randperm(pool_pages, generator=g).to(torch.int32).to(dev)
+    pools = torch.ones(2 * pool_pages * 32768, dtype=torch.uint8, device=dev)
+    k, v = pools[:pool_pages * 32768], pools[pool_pages * 32768:]
+    grid = 512
+    sink = torch.zeros(grid * 256, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def timed(fn):
+        def call(_):
+            rc = fn()
+            if rc != 0:
+                raise RuntimeError(f"read probe launch failed: {rc}")
+        return event_time_ms(call, 5, 2)
+
+    res = {"workload": "2 GiB of 32 KB pages, chains of 64 seeded-permutation pages, 512 workgroups"}
+    for name, hpu in (("one_kv_head_256B_rows", 1), ("whole_2KB_rows", 8)):
+        ms = timed(lambda: lib.fe_probe_rows(pools.data_ptr(), perm2.data_ptr(), 2 * pool_pages // chain, chain,
+                                             hpu, grid, sink.data_ptr(), st))
+        res[name] = {"ms": round(ms, 4), "gbs": round(pools.numel() / ms / 1e6, 1)}
+    ms = timed(lambda: lib.fe_probe_tile_copy(k.data_ptr(), v.data_ptr(), perm1.data_ptr(), pool_pages // chain,
+                                              chain, grid, sink.data_ptr(), st))
+    res["tile_kernel_copy_stream"] = {"ms": round(ms, 4), "gbs": round(pools.numel() / ms / 1e6, 1)}
+    del pools, k, v
+    return res
+
+
 def host_cpu():
     """The host the CPU baseline runs on: model name from /proc/cpuinfo, the
     CPUs this process may run on (what `nproc` reports), os.cpu_count() and
@@ -394,7 +446,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph"],
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern"],
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:
