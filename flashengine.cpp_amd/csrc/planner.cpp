@@ -121,40 +121,31 @@ bool cut_tile_stream(const std::vector<SeqInfo>& seqs, int G, int hkv, bool caus
     }
   }
   if (ch.empty()) return false;
-  const int64_t quota = (total + n_shares - 1) / n_shares;
-  // Pieces in stream order: (chunk, first tile, tiles, share); the last share
-  // takes whatever rounding leaves over.
+  // Pieces in stream order: (chunk, first tile, tiles, share).  Share k ends
+  // at the first tile boundary where the cumulative cost reaches
+  // (k + 1) * total / n_shares, so a tile's granularity never accumulates
+  // from share to share; the last share ends with the stream.
   struct Piece {
     int chunk, tile0, ntiles, share;
   };
   std::vector<Piece> pcs;
   std::vector<int> npc(ch.size(), 0);
   int share = 0;
-  int64_t load = 0;
+  int64_t cum = 0;
+  auto target = [&](int k) { return ((int64_t)(k + 1) * total + n_shares - 1) / n_shares; };
   for (int i = 0; i < (int)ch.size(); ++i) {
     int done = 0;
     while (done < ch[i].tiles) {
+      while (share < n_shares - 1 && cum >= target(share)) ++share;
       int take = ch[i].tiles - done;
       if (share < n_shares - 1) {
-        int64_t room = (quota - load) / ch[i].c;
-        if (room <= 0) {
-          if (load > 0) {
-            ++share;
-            load = 0;
-            continue;
-          }
-          room = 1;
-        }
-        take = (int)std::min<int64_t>(room, take);
+        const int64_t need = (target(share) - cum + ch[i].c - 1) / ch[i].c;  // >= 1 tile
+        take = (int)std::min<int64_t>(need, take);
       }
       pcs.push_back(Piece{i, done, take, share});
       ++npc[i];
       done += take;
-      load += (int64_t)take * ch[i].c;
-      if (share < n_shares - 1 && load >= quota) {
-        ++share;
-        load = 0;
-      }
+      cum += (int64_t)take * ch[i].c;
     }
   }
   if ((int64_t)pcs.size() * hkv > item_cap) return false;

@@ -100,6 +100,30 @@ def test_tile_stream_cut_balances_block_verify():
     assert len(loads) <= 64 and max(loads) <= quota
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (40, 5), (32, 16)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_tile_stream_cut_balances_chunks(hq, hkv, causal):
+    """Chunks of one and two 16-column blocks per wavefront over long
+    prefixes, few enough that the longest-first list splits them: the equal
+    cut is used, and no share exceeds its exact part of the stream by more
+    than one tile step (cost 2) -- the tile granularity must not pile up on
+    the last share."""
+    b = W.make_batch(hq, hkv, starts=[6000, 9000, 300], qlens=[200, 64, 40], seed=hq + hkv)
+    items = [it for it in coverage(b, causal) if it[0] == 1]
+    runs = []
+    for it in items:
+        if runs and runs[-1][0] == it[4]:
+            runs[-1][1].append(it)
+        else:
+            runs.append((it[4], [it]))
+    assert [h for h, _ in runs] == list(range(hkv)) * (len(runs) // hkv)
+    cost = lambda x: ((x[6] - x[5] + 63) // 64) * (2 if x[3] * b.group > 64 else 1)
+    loads = [sum(cost(x) for x in runs[k][1]) for k in range(0, len(runs), hkv)]
+    shares = 512 // hkv
+    assert len(loads) <= shares
+    assert max(loads) <= -(-sum(loads) // shares) + 1
+
+
 def test_split_kv_produces_merges():
     b = W.long_decode(batch=4, ctx=32768)
     counts = feattn.describe(*plan_args(b))
