@@ -85,6 +85,9 @@ CASES = [
     (64, 2, [1500, 40], [1, 2]),                             # GQA 32
     (128, 1, [800, 20], [1, 2]),                             # GQA 128: one row is a whole tile item
     (32, 16, [1200, 3, 600], [1, 9, 70]),                    # hkv 16: a decode share spans two workgroups
+    (32, 8, [6000, 9000, 300], [200, 64, 40]),               # tile stream cut: one- and two-block chunks
+    (40, 5, [7000, 2500, 12000], [48, 20, 33]),              # tile stream cut over 102 shares per kv head
+    (32, 8, [3000, 7000, 11000, 1500], [16, 16, 16, 16]),    # tile stream cut: 16-row blocks
 ]
 
 

@@ -178,3 +178,41 @@ def test_exact_counts_long_chunks(dev, causal):
     tiles, splits and merges across many tile items."""
     b = W.make_batch(32, 8, starts=[0, 3000], qlens=[8192, 2048], seed=81, extra_pages=1)
     run_case(dev, b, causal, "f16")
+
+
+# Batches whose tile work is the equal cut of the tile stream (the
+# longest-first list would split their chunks): one- and two-block chunks
+# over long prefixes, 5 and 16 kv heads, one query head per kv head, and
+# 16-row blocks; every piece boundary falls inside a chunk.
+STREAM_CUT = {
+    "chunks_32_8": (32, 8, [6000, 9000, 300], [200, 64, 40]),
+    "chunks_40_5": (40, 5, [7000, 2500, 12000], [48, 20, 33]),
+    "chunks_8_8": (8, 8, [9000, 4000], [300, 130]),
+    "chunks_32_16": (32, 16, [10000, 3000, 5000], [100, 70, 17]),
+    "blocks_32_8": (32, 8, [3000, 7000, 11000, 1500, 9000, 5000], [16] * 6),
+}
+
+
+def stream_cut_taken(b, causal):
+    """True when the tile list is laid out as the equal cut: kv heads in
+    runs 0..hkv-1 repeating, kv head 0's pieces following the tile stream,
+    and some chunk cut into consecutive pieces."""
+    items = [it for it in feattn.dump(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), b.blocks, b.qo, b.kv,
+                                      b.pages, b.last, b.batch, b.rows, causal) if it[0] == 1]
+    heads = [it[4] for i, it in enumerate(items) if i == 0 or it[4] != items[i - 1][4]]
+    if heads != list(range(b.hkv)) * (len(heads) // b.hkv):
+        return False
+    k0 = [it for it in items if it[4] == 0]
+    if not any((a[1], a[2]) == (c[1], c[2]) for a, c in zip(k0, k0[1:])):
+        return False
+    return all((c[1], c[2], c[5]) == ((a[1], a[2], a[6]) if a[6] < c[6] and (a[1], a[2]) == (c[1], c[2])
+                                      else (c[1], c[2], 0)) for a, c in zip(k0, k0[1:]))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("name", list(STREAM_CUT))
+def test_exact_counts_tile_stream_cut(dev, name, causal):
+    hq, hkv, starts, qlens = STREAM_CUT[name]
+    b = W.make_batch(hq, hkv, starts=starts, qlens=qlens, seed=hq + hkv + 5, extra_pages=1)
+    assert stream_cut_taken(b, causal)
+    run_case(dev, b, causal, "f16")
