@@ -12,7 +12,8 @@ value = algorithmic decode bytes per step (visible K/V rows + q in + o out +
 page ids) / measured time per step, in GB/s.  Secondary figures (chunked
 prefill TFLOP/s, fused RoPE+append GB/s, DFlash block, mixed step,
 long-context decode) are reported under "secondary"; `--only pattern` prints
-the read throughput of the cache access patterns alone (lib/libfeprobe.so).
+the read throughput of the cache access patterns alone and `--only issue` the
+MFMA / VALU issue overlap (reference kernels in lib/libfeprobe.so).
 The CPU baseline is the oracle's LibTorch-CPU restatement of the reference's
 ATen attention on the same decode batch.
 
@@ -124,7 +125,7 @@ def decode_headline(steps, warmup, dev):
 
 def secondary(dev, only=None):
     """Other workload shapes: ms per call and throughput.  `only` selects one
-    of prefill / dflash / mixed / long / graph / pattern."""
+    of prefill / dflash / mixed / long / graph / pattern / issue."""
     import torch
 
     import feattn
@@ -150,6 +151,9 @@ def secondary(dev, only=None):
     if only == "pattern":  # reference figures, not part of the default run
         res["read_patterns"] = read_patterns(dev)
         log("read patterns", res["read_patterns"])
+    if only == "issue":
+        res["issue_overlap"] = issue_overlap(dev)
+        log("issue overlap", res["issue_overlap"])
     return res
 
 
@@ -365,6 +369,44 @@ def read_patterns(dev):
     return res
 
 
+def issue_overlap(dev):
+    """Shader-clock cycles per (one 16x16x32 bf16 MFMA + K independent VALU
+    instructions) of lib/libfeprobe.so's issue probe, median over
+    wavefronts, with one and with two wavefronts per SIMD.  One wavefront:
+    cycles ~ MFMA + K x VALU means it never overlaps its own MFMA and VALU
+    work; two: the per-SIMD cycles show how much of one wavefront's MFMA the
+    other's VALU work hides."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
+    lib = ctypes.CDLL(path)
+    lib.fe_probe_issue.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    st = torch.cuda.current_stream().cuda_stream
+    iters = 20000
+    res = {"workload": f"{iters} x 4 MFMA chains per wavefront, K VALU after each MFMA; cycles by s_memtime"}
+    for per_simd in (1, 2):
+        grid = 4 * cus * per_simd
+        sink = torch.zeros(grid * 64, device=dev)
+        row = {}
+        for op, ks in (("fma", (2, 4, 8, 16)), ("exp", (2, 4))):
+            for k in ks:
+                for _ in range(2):  # the second launch is kept (clock settled)
+                    if lib.fe_probe_issue(sink.data_ptr(), iters, k, op == "exp", grid, st) != 0:
+                        raise RuntimeError("issue probe launch failed")
+                torch.cuda.synchronize()
+                cyc = statistics.median(sink.view(grid, 64)[:, 0].cpu().tolist()) / (iters * 4)
+                row[f"{op}_K{k}"] = {"per_wavefront": round(cyc, 2), "per_simd": round(cyc / per_simd, 2)}
+        res[f"{per_simd}_wavefront_per_simd"] = row
+        del sink
+    return res
+
+
 def host_cpu():
     """The host the CPU baseline runs on: model name from /proc/cpuinfo, the
     CPUs this process may run on (what `nproc` reports), os.cpu_count() and
@@ -446,7 +488,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern"],
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern", "issue"],
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:

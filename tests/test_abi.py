@@ -81,11 +81,11 @@ def test_error_reporting_without_device():
 
 
 def test_read_probe_library_is_separate():
-    """The benchmark's read-pattern kernels live in their own library: it
-    exports its two launchers, and the attention library exports neither."""
+    """The benchmark's reference kernels live in their own library: it
+    exports its launchers, and the attention library exports none of them."""
     probe = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
     out = subprocess.run(["nm", "-D", "--defined-only", probe], capture_output=True, text=True,
                          check=True).stdout
-    for name in ("fe_probe_rows", "fe_probe_tile_copy"):
+    for name in ("fe_probe_rows", "fe_probe_tile_copy", "fe_probe_issue"):
         assert re.search(rf"\bT {name}\b", out), name
         assert not hasattr(feattn.lib(), name), name
