@@ -182,14 +182,17 @@ def test_exact_counts_long_chunks(dev, causal):
 
 # Batches whose tile work is the equal cut of the tile stream (the
 # longest-first list would split their chunks): one- and two-block chunks
-# over long prefixes, 5 and 16 kv heads, one query head per kv head, and
-# 16-row blocks; every piece boundary falls inside a chunk.
+# over long prefixes, 5, 4 and 16 kv heads, one query head per kv head, one
+# kv head for 128 query heads (a chunk is one row), and 16-row blocks; every
+# piece boundary falls inside a chunk.
 STREAM_CUT = {
     "chunks_32_8": (32, 8, [6000, 9000, 300], [200, 64, 40]),
     "chunks_40_5": (40, 5, [7000, 2500, 12000], [48, 20, 33]),
     "chunks_8_8": (8, 8, [9000, 4000], [300, 130]),
     "chunks_32_16": (32, 16, [10000, 3000, 5000], [100, 70, 17]),
     "blocks_32_8": (32, 8, [3000, 7000, 11000, 1500, 9000, 5000], [16] * 6),
+    "rows_128_1": (128, 1, [9000, 3000], [40, 20]),
+    "chunks_64_4": (64, 4, [12000, 800], [50, 30]),
 }
 
 
