@@ -14,6 +14,7 @@ import torch
 
 import feattn
 from feattn import workloads as W
+from test_gpu_known_counts import stream_cut_taken
 from oracle import aten_attention as A
 
 pytestmark = pytest.mark.gpu
@@ -219,7 +220,9 @@ def test_graph_captured_on_blocks(dev):
     other block batches and single-row batches, each matching the oracle,
     and refuses 8-row items, which need the wider decode variant than the
     one captured (reference refusal of layout changes:
-    src/flashinfer_attention.cu:32)."""
+    src/flashinfer_attention.cu:32).  The two block batches are planned one
+    by the longest-first list and one by the equal cut of the tile stream,
+    so the replays switch between the two share layouts."""
     hq, hkv, blocks = 32, 8, 900
     kc = torch.zeros(blocks + 1, 16, hkv, 128, dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
@@ -251,6 +254,7 @@ def test_graph_captured_on_blocks(dev):
     steps = [first,
              W.make_batch(hq, hkv, starts=[3500, 5, 700, 1800], qlens=[16] * 4, seed=2, pool=blocks),
              W.make_batch(hq, hkv, starts=[3000, 5, 700, 1800], qlens=[1] * 4, seed=3, pool=blocks)]
+    assert not stream_cut_taken(steps[0], False) and stream_cut_taken(steps[1], False)
     for seed, bb in enumerate(steps, start=1):
         qq, kk, vv = load(bb, seed)
         graph.replay()
