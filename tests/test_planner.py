@@ -237,3 +237,52 @@ def test_share_assignment_rejects_bad_input():
         feattn.assign_shares([3, -1], 4)
     with pytest.raises(RuntimeError, match="slots"):
         feattn.assign_shares([3], 0)
+
+
+@pytest.mark.parametrize("shape", ["blocks", "chunks", "rows_128_1", "split_decode"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_partial_slots_are_laid_out_for_the_merge(shape, causal):
+    """Split-KV bookkeeping of the tile lists (longest-first or stream cut):
+    every (partial slot, kv head) is written by exactly one piece, a row cut
+    into n pieces owns slots base + s * nq (s < n, in token order) with the
+    same base for every kv head, unsplit rows own none, and the slots in use
+    are exactly [decode partials, partial rows) (no slot left unused)."""
+    if shape == "blocks":
+        b = W.make_batch(32, 8, starts=[3000, 7000, 11000, 1500, 9000, 5000], qlens=[16] * 6, seed=4)
+    elif shape == "chunks":
+        b = W.make_batch(32, 8, starts=[6000, 9000, 300], qlens=[200, 64, 40], seed=5)
+    elif shape == "rows_128_1":
+        b = W.make_batch(128, 1, starts=[9000, 3000], qlens=[40, 20], seed=6)
+    else:
+        b = W.make_batch(32, 8, starts=[20000, 6000, 300, 12000], qlens=[1, 64, 1, 16], seed=7)
+    items = feattn.dump(*plan_args(b), causal=causal)
+    d, t, m, p = feattn.describe(*plan_args(b))
+    tile = [it for it in items if it[0] == 1]
+    dec = [it for it in items if it[0] == 0]
+    dec_slots = {it[7] + r for it in dec if it[7] >= 0 for r in range(it[3])}
+    base = max(dec_slots) + 1 if dec_slots else 0
+    owner = {}
+    pieces = {}
+    for kind, seq, q0, nq, kvh, t0, t1, part in tile:
+        for r in range(nq):
+            pieces.setdefault((q0 + r, kvh), []).append((t0, part + r if part >= 0 else -1))
+            if part >= 0:
+                key = (part + r, kvh)
+                assert key not in owner, key
+                owner[key] = (q0 + r, t0)
+    used = set()
+    for (row, kvh), ps in pieces.items():
+        ps.sort()
+        if len(ps) == 1:
+            assert ps[0][1] == -1, (row, kvh)
+            continue
+        slots = [s for _, s in ps]
+        assert all(s >= 0 for s in slots)
+        stride = slots[1] - slots[0]
+        assert stride > 0 and slots == [slots[0] + i * stride for i in range(len(slots))], (row, kvh)
+        assert pieces[(row, 0)] and [s for _, s in sorted(pieces[(row, 0)])] == slots  # same for every kv head
+        used.update(slots)
+    assert used  # every shape here splits tile rows
+    assert min(used) == base and len(used) == max(used) - base + 1
+    if causal:  # describe() counts the causal lists
+        assert max(used) == p - 1
