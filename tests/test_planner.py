@@ -239,22 +239,13 @@ def test_share_assignment_rejects_bad_input():
         feattn.assign_shares([3], 0)
 
 
-@pytest.mark.parametrize("shape", ["blocks", "chunks", "rows_128_1", "split_decode"])
-@pytest.mark.parametrize("causal", [True, False])
-def test_partial_slots_are_laid_out_for_the_merge(shape, causal):
+def check_partial_slots(b, causal):
     """Split-KV bookkeeping of the tile lists (longest-first or stream cut):
     every (partial slot, kv head) is written by exactly one piece, a row cut
     into n pieces owns slots base + s * nq (s < n, in token order) with the
     same base for every kv head, unsplit rows own none, and the slots in use
-    are exactly [decode partials, partial rows) (no slot left unused)."""
-    if shape == "blocks":
-        b = W.make_batch(32, 8, starts=[3000, 7000, 11000, 1500, 9000, 5000], qlens=[16] * 6, seed=4)
-    elif shape == "chunks":
-        b = W.make_batch(32, 8, starts=[6000, 9000, 300], qlens=[200, 64, 40], seed=5)
-    elif shape == "rows_128_1":
-        b = W.make_batch(128, 1, starts=[9000, 3000], qlens=[40, 20], seed=6)
-    else:
-        b = W.make_batch(32, 8, starts=[20000, 6000, 300, 12000], qlens=[1, 64, 1, 16], seed=7)
+    are [decode partials, partial rows) with none left unused.  Returns the
+    slots in use."""
     items = feattn.dump(*plan_args(b), causal=causal)
     d, t, m, p = feattn.describe(*plan_args(b))
     tile = [it for it in items if it[0] == 1]
@@ -280,9 +271,47 @@ def test_partial_slots_are_laid_out_for_the_merge(shape, causal):
         assert all(s >= 0 for s in slots)
         stride = slots[1] - slots[0]
         assert stride > 0 and slots == [slots[0] + i * stride for i in range(len(slots))], (row, kvh)
-        assert pieces[(row, 0)] and [s for _, s in sorted(pieces[(row, 0)])] == slots  # same for every kv head
+        assert [s for _, s in sorted(pieces[(row, 0)])] == slots  # same for every kv head
         used.update(slots)
-    assert used  # every shape here splits tile rows
-    assert min(used) == base and len(used) == max(used) - base + 1
-    if causal:  # describe() counts the causal lists
-        assert max(used) == p - 1
+    if used:
+        assert min(used) == base and len(used) == max(used) - base + 1
+        if causal:  # describe() counts the causal lists
+            assert max(used) == p - 1
+    return used
+
+
+@pytest.mark.parametrize("shape", ["blocks", "chunks", "rows_128_1", "split_decode"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_partial_slots_are_laid_out_for_the_merge(shape, causal):
+    if shape == "blocks":
+        b = W.make_batch(32, 8, starts=[3000, 7000, 11000, 1500, 9000, 5000], qlens=[16] * 6, seed=4)
+    elif shape == "chunks":
+        b = W.make_batch(32, 8, starts=[6000, 9000, 300], qlens=[200, 64, 40], seed=5)
+    elif shape == "rows_128_1":
+        b = W.make_batch(128, 1, starts=[9000, 3000], qlens=[40, 20], seed=6)
+    else:
+        b = W.make_batch(32, 8, starts=[20000, 6000, 300, 12000], qlens=[1, 64, 1, 16], seed=7)
+    assert check_partial_slots(b, causal)  # every shape here splits tile rows
+
+
+HEAD_LAYOUTS = [(32, 8), (16, 2), (40, 5), (64, 4), (8, 8), (128, 1), (24, 6), (32, 16), (48, 8), (96, 32)]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_batches_cover_and_lay_out_partials(seed):
+    """Seeded random ragged batches (head layout, batch size, decode rows,
+    short blocks and longer chunks, prefixes up to 6000 tokens): every
+    visible (row, kv head, token) is covered exactly once with both masks,
+    and the partial slots of split rows are laid out for the merge."""
+    rng = np.random.default_rng(1000 + seed)
+    hq, hkv = HEAD_LAYOUTS[seed % len(HEAD_LAYOUTS)]
+    batch = int(rng.integers(1, 9))
+    qlens, starts = [], []
+    for _ in range(batch):
+        kind = rng.integers(0, 3)
+        qlens.append(int(1 if kind == 0 else rng.integers(2, 33) if kind == 1 else rng.integers(33, 161)))
+        starts.append(int(rng.integers(0, 6001)))
+    b = W.make_batch(hq, hkv, starts=starts, qlens=qlens, seed=seed, extra_pages=int(rng.integers(0, 3)))
+    for causal in (True, False):
+        coverage(b, causal)
+        check_partial_slots(b, causal)
