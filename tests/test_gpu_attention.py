@@ -258,3 +258,27 @@ def test_matches_reference_aten_on_device(dev, causal):
         ref = ref_lib.attention(b, q, kc, vc, causal).cpu()
         out, _ = hip_attention(b, q, kc, vc, causal, dev)
         torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_batches_vs_oracle(dev, seed):
+    """Seeded random ragged batches (the planner's random-batch generator:
+    head layout, decode rows, short blocks, longer chunks, prefixes up to
+    6000 tokens) through both masks against the oracle; between them they
+    take the longest-first list, the stream cut, split and unsplit rows."""
+    from test_planner import HEAD_LAYOUTS
+
+    rng = np.random.default_rng(1000 + seed)
+    hq, hkv = HEAD_LAYOUTS[seed % len(HEAD_LAYOUTS)]
+    batch = int(rng.integers(1, 9))
+    qlens, starts = [], []
+    for _ in range(batch):
+        kind = rng.integers(0, 3)
+        qlens.append(int(1 if kind == 0 else rng.integers(2, 33) if kind == 1 else rng.integers(33, 161)))
+        starts.append(int(rng.integers(0, 6001)))
+    b = W.make_batch(hq, hkv, starts=starts, qlens=qlens, seed=seed, extra_pages=int(rng.integers(0, 3)))
+    q, kc, vc = W.make_tensors(b, seed=500 + seed)
+    for causal in (True, False):
+        want_out, want_lse = A.run(b, q, kc, vc, causal)
+        out, lse = hip_attention(b, q, kc, vc, causal, dev)
+        check(out, lse, want_out, want_lse)
