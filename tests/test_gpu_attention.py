@@ -260,7 +260,7 @@ def test_matches_reference_aten_on_device(dev, causal):
         torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_random_batches_vs_oracle(dev, seed):
     """Seeded random ragged batches (the planner's random-batch generator:
     head layout, decode rows, short blocks, longer chunks, prefixes up to
