@@ -12,8 +12,9 @@ value = algorithmic decode bytes per step (visible K/V rows + q in + o out +
 page ids) / measured time per step, in GB/s.  Secondary figures (chunked
 prefill TFLOP/s, fused RoPE+append GB/s, DFlash block, mixed step,
 long-context decode) are reported under "secondary"; `--only pattern` prints
-the read throughput of the cache access patterns alone and `--only issue` the
-MFMA / VALU issue overlap (reference kernels in lib/libfeprobe.so).
+the read throughput of the cache access patterns alone, `--only issue` the
+MFMA / VALU issue overlap and `--only lds` the LDS read throughput
+(reference kernels in lib/libfeprobe.so).
 The CPU baseline is the oracle's LibTorch-CPU restatement of the reference's
 ATen attention on the same decode batch.
 
@@ -125,7 +126,7 @@ def decode_headline(steps, warmup, dev):
 
 def secondary(dev, only=None):
     """Other workload shapes: ms per call and throughput.  `only` selects one
-    of prefill / dflash / mixed / long / graph / pattern / issue."""
+    of prefill / dflash / mixed / long / graph / pattern / issue / lds."""
     import torch
 
     import feattn
@@ -154,6 +155,9 @@ def secondary(dev, only=None):
     if only == "issue":
         res["issue_overlap"] = issue_overlap(dev)
         log("issue overlap", res["issue_overlap"])
+    if only == "lds":
+        res["lds_throughput"] = lds_throughput(dev)
+        log("lds throughput", res["lds_throughput"])
     return res
 
 
@@ -407,6 +411,41 @@ def issue_overlap(dev):
     return res
 
 
+def lds_throughput(dev):
+    """LDS read bytes per shader clock per CU of lib/libfeprobe.so's LDS
+    probe (one workgroup of W wavefronts per CU, 8 independent reads then a
+    wait, bank-conflict-free addresses), for the tile kernel's two operand
+    reads: ds_read_b128 (K) and ds_read_b64_tr_b16 (V^T).  Median over
+    workgroups."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
+    lib = ctypes.CDLL(path)
+    lib.fe_probe_lds.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    st = torch.cuda.current_stream().cuda_stream
+    iters = 20000
+    res = {"workload": f"{iters} x 8 reads per wavefront, one workgroup per CU; bytes per clock per CU"}
+    for name, tr, per_read in (("ds_read_b128", 0, 1024), ("ds_read_b64_tr_b16", 1, 512)):
+        row = {}
+        for waves in (4, 8, 16):
+            sink = torch.zeros(cus * 64 * waves, device=dev)
+            for _ in range(2):  # the second launch is kept
+                if lib.fe_probe_lds(sink.data_ptr(), iters, waves, tr, cus, st) != 0:
+                    raise RuntimeError("LDS probe launch failed")
+            torch.cuda.synchronize()
+            cyc = statistics.median(sink.view(cus, 64 * waves)[:, 0].cpu().tolist())
+            row[f"{waves}_wavefronts"] = round(waves * 8 * per_read * iters / cyc, 1)
+            del sink
+        res[name] = row
+    return res
+
+
 def host_cpu():
     """The host the CPU baseline runs on: model name from /proc/cpuinfo, the
     CPUs this process may run on (what `nproc` reports), os.cpu_count() and
@@ -488,7 +527,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern", "issue"],
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern", "issue", "lds"],
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -86,6 +86,6 @@ def test_read_probe_library_is_separate():
     probe = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
     out = subprocess.run(["nm", "-D", "--defined-only", probe], capture_output=True, text=True,
                          check=True).stdout
-    for name in ("fe_probe_rows", "fe_probe_tile_copy", "fe_probe_issue"):
+    for name in ("fe_probe_rows", "fe_probe_tile_copy", "fe_probe_issue", "fe_probe_lds"):
         assert re.search(rf"\bT {name}\b", out), name
         assert not hasattr(feattn.lib(), name), name
