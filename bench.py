@@ -11,10 +11,7 @@ so the 256 MB Infinity Cache cannot hold the working set.
 value = algorithmic decode bytes per step (visible K/V rows + q in + o out +
 page ids) / measured time per step, in GB/s.  Secondary figures (chunked
 prefill TFLOP/s, fused RoPE+append GB/s, DFlash block, mixed step,
-long-context decode) are reported under "secondary"; `--only pattern` prints
-the read throughput of the cache access patterns alone, `--only issue` the
-MFMA / VALU issue overlap and `--only lds` the LDS read throughput
-(reference kernels in lib/libfeprobe.so).
+long-context decode) are reported under "secondary".
 The CPU baseline is the oracle's LibTorch-CPU restatement of the reference's
 ATen attention on the same decode batch.
 
@@ -126,7 +123,7 @@ def decode_headline(steps, warmup, dev):
 
 def secondary(dev, only=None):
     """Other workload shapes: ms per call and throughput.  `only` selects one
-    of prefill / dflash / mixed / long / graph / pattern / issue / lds."""
+    of prefill / dflash / mixed / long / graph."""
     import torch
 
     import feattn
@@ -149,15 +146,6 @@ def secondary(dev, only=None):
         _long(dev, res)
     if want("graph"):
         _graph(dev, res)
-    if only == "pattern":  # reference figures, not part of the default run
-        res["read_patterns"] = read_patterns(dev)
-        log("read patterns", res["read_patterns"])
-    if only == "issue":
-        res["issue_overlap"] = issue_overlap(dev)
-        log("issue overlap", res["issue_overlap"])
-    if only == "lds":
-        res["lds_throughput"] = lds_throughput(dev)
-        log("lds throughput", res["lds_throughput"])
     return res
 
 
@@ -325,127 +313,6 @@ def copy_calibration(dev, mib=1024):
     return {"bytes_per_copy": 2 * n, "ms": round(ms, 4), "gbs": round(2 * n / ms / 1e6, 1)}
 
 
-def read_patterns(dev):
-    """Read throughput of the cache access patterns alone (lib/libfeprobe.so,
-    no attention arithmetic): 2 GiB of 32 KB pages (16 rows of 8 kv heads x
-    256 B) in seeded-permutation chains of 64 pages; one kv head's 256 B of
-    every row per work unit (as a tile workgroup reads the cache), whole 2 KB
-    rows (as a decode workgroup's wavefronts read it together), and the tile
-    kernel's copy stream (K and V pools of 1 GiB each, direct-to-LDS copies,
-    one 64-token tile in flight per workgroup) without its compute."""
-    import ctypes
-
-    import torch
-
-    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
-    lib = ctypes.CDLL(path)
-    vp, i = ctypes.c_void_p, ctypes.c_int
-    lib.fe_probe_rows.argtypes = [vp, vp, i, i, i, i, vp, vp]
-    lib.fe_probe_tile_copy.argtypes = [vp, vp, vp, i, i, i, vp, vp]
-    pool_pages, chain = 32768, 64
-    g = torch.Generator().manual_seed(7)
-    perm2 = torch.randperm(2 * pool_pages, generator=g).to(torch.int32).to(dev)
-    perm1 = torch.randperm(pool_pages, generator=g).to(torch.int32).to(dev)
-    pools = torch.ones(2 * pool_pages * 32768, dtype=torch.uint8, device=dev)
-    k, v = pools[:pool_pages * 32768], pools[pool_pages * 32768:]
-    grid = 512
-    sink = torch.zeros(grid * 256, dtype=torch.int32, device=dev)
-    st = torch.cuda.current_stream().cuda_stream
-
-    def timed(fn):
-        def call(_):
-            rc = fn()
-            if rc != 0:
-                raise RuntimeError(f"read probe launch failed: {rc}")
-        return event_time_ms(call, 5, 2)
-
-    res = {"workload": "2 GiB of 32 KB pages, chains of 64 seeded-permutation pages, 512 workgroups"}
-    for name, hpu in (("one_kv_head_256B_rows", 1), ("whole_2KB_rows", 8)):
-        ms = timed(lambda: lib.fe_probe_rows(pools.data_ptr(), perm2.data_ptr(), 2 * pool_pages // chain, chain,
-                                             hpu, grid, sink.data_ptr(), st))
-        res[name] = {"ms": round(ms, 4), "gbs": round(pools.numel() / ms / 1e6, 1)}
-    ms = timed(lambda: lib.fe_probe_tile_copy(k.data_ptr(), v.data_ptr(), perm1.data_ptr(), pool_pages // chain,
-                                              chain, grid, sink.data_ptr(), st))
-    res["tile_kernel_copy_stream"] = {"ms": round(ms, 4), "gbs": round(pools.numel() / ms / 1e6, 1)}
-    del pools, k, v
-    return res
-
-
-def issue_overlap(dev):
-    """Shader-clock cycles per (one 16x16x32 bf16 MFMA + K independent VALU
-    instructions) of lib/libfeprobe.so's issue probe, median over
-    wavefronts, with one and with two wavefronts per SIMD.  One wavefront:
-    cycles ~ MFMA + K x VALU means it never overlaps its own MFMA and VALU
-    work; two: the per-SIMD cycles show how much of one wavefront's MFMA the
-    other's VALU work hides."""
-    import ctypes
-
-    import torch
-
-    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
-    lib = ctypes.CDLL(path)
-    lib.fe_probe_issue.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                   ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    st = torch.cuda.current_stream().cuda_stream
-    iters = 20000
-    res = {"workload": f"{iters} x 4 MFMA chains per wavefront, K VALU after each MFMA; cycles by s_memtime"}
-    for per_simd in (1, 2):
-        grid = 4 * cus * per_simd
-        sink = torch.zeros(grid * 64, device=dev)
-        row = {}
-        for op, ks in (("fma", (2, 4, 8, 16)), ("exp", (2, 4))):
-            for k in ks:
-                for _ in range(2):  # the second launch is kept (clock settled)
-                    if lib.fe_probe_issue(sink.data_ptr(), iters, k, op == "exp", grid, st) != 0:
-                        raise RuntimeError("issue probe launch failed")
-                torch.cuda.synchronize()
-                cyc = statistics.median(sink.view(grid, 64)[:, 0].cpu().tolist()) / (iters * 4)
-                row[f"{op}_K{k}"] = {"per_wavefront": round(cyc, 2), "per_simd": round(cyc / per_simd, 2)}
-        res[f"{per_simd}_wavefront_per_simd"] = row
-        del sink
-    return res
-
-
-def lds_throughput(dev):
-    """LDS read bytes per shader clock per CU of lib/libfeprobe.so's LDS
-    probe (one workgroup of W wavefronts per CU, 8 independent reads then a
-    wait, bank-conflict-free addresses), for the tile kernel's two operand
-    reads: ds_read_b128 (K) and ds_read_b64_tr_b16 (V^T).  Median over
-    workgroups."""
-    import ctypes
-
-    import torch
-
-    path = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is missing: build it with `make -C flashengine.cpp_amd`")
-    lib = ctypes.CDLL(path)
-    lib.fe_probe_lds.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                 ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    st = torch.cuda.current_stream().cuda_stream
-    iters = 20000
-    res = {"workload": f"{iters} x 8 reads per wavefront, one workgroup per CU; bytes per clock per CU"}
-    for name, tr, per_read in (("ds_read_b128", 0, 1024), ("ds_read_b64_tr_b16", 1, 512)):
-        row = {}
-        for waves in (4, 8, 16):
-            sink = torch.zeros(cus * 64 * waves, device=dev)
-            for _ in range(2):  # the second launch is kept
-                if lib.fe_probe_lds(sink.data_ptr(), iters, waves, tr, cus, st) != 0:
-                    raise RuntimeError("LDS probe launch failed")
-            torch.cuda.synchronize()
-            cyc = statistics.median(sink.view(cus, 64 * waves)[:, 0].cpu().tolist())
-            row[f"{waves}_wavefronts"] = round(waves * 8 * per_read * iters / cyc, 1)
-            del sink
-        res[name] = row
-    return res
-
-
 def host_cpu():
     """The host the CPU baseline runs on: model name from /proc/cpuinfo, the
     CPUs this process may run on (what `nproc` reports), os.cpu_count() and
@@ -527,7 +394,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph", "pattern", "issue", "lds"],
+    ap.add_argument("--only", choices=["prefill", "dflash", "mixed", "long", "graph"],
                     help="run one secondary workload only (for profiling); no headline line")
     args = ap.parse_args()
     if args.gpus != 1:

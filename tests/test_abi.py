@@ -79,13 +79,3 @@ def test_error_reporting_without_device():
     rc = lib.fe_attn_plan_create(30, 8, 128, 16, 4, 4, 1, 16, ctypes.byref(h))
     assert rc == feattn.FE_EINVAL
 
-
-def test_read_probe_library_is_separate():
-    """The benchmark's reference kernels live in their own library: it
-    exports its launchers, and the attention library exports none of them."""
-    probe = os.path.join(ROOT, "flashengine.cpp_amd", "lib", "libfeprobe.so")
-    out = subprocess.run(["nm", "-D", "--defined-only", probe], capture_output=True, text=True,
-                         check=True).stdout
-    for name in ("fe_probe_rows", "fe_probe_tile_copy", "fe_probe_issue", "fe_probe_lds"):
-        assert re.search(rf"\bT {name}\b", out), name
-        assert not hasattr(feattn.lib(), name), name
