@@ -52,6 +52,24 @@ def measured_traffic():
     return None
 
 
+def event_block_means_ms(fn, blocks, iters):
+    """Mean ms per call of each of `blocks` consecutive blocks of `iters`
+    calls, one event between blocks on the current stream (an event marker
+    between single launches adds about 2 us to each, so the statistic is
+    taken over blocks)."""
+    import torch
+
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
+    ev[0].record()
+    for j in range(blocks):
+        for i in range(iters):
+            fn(j * iters + i)
+        ev[j + 1].record()
+    torch.cuda.synchronize()
+    return [ev[j].elapsed_time(ev[j + 1]) / iters for j in range(blocks)]
+
+
 def event_time_ms(fn, iters, warmup):
     """Average ms per call of fn() over `iters` calls, timed with events on
     the current stream (the stream the library launches on)."""
@@ -87,6 +105,52 @@ def make_pools(b, n, dev, dtype):
     return pools
 
 
+ROPE_THETA = 1e6  # Qwen3
+
+
+def make_rope_pools(b, n, dev):
+    """Decode pools filled the way the engine fills them: for every context
+    token, raw q / k / v ~ N(0,1) (bf16), k and q rotated at the token's
+    position with theta 1e6 and k / v written to the token's page slot by
+    the fused RoPE + paged append (src/cuda_model.cpp:94-95), the RoPE table
+    built on the device (src/cuda_model.cpp:44-47).  Returns the pools and
+    the decode query rows: q of each sequence's last token, rotated at
+    position len - 1.  Slots outside every sequence (page tails, the dummy
+    page) hold zeros and are never read."""
+    import torch
+
+    import feattn
+    from feattn import workloads as W
+
+    fill = W.Batch(hq=b.hq, hkv=b.hkv, page=b.page, blocks=b.blocks, starts=[0] * b.batch,
+                   qlens=list(b.lens), tables=b.tables)
+    W.build_metadata(fill)
+    rows = fill.rows
+    max_pos = max(b.lens)
+    table = torch.empty(max_pos, 128, device=dev)
+    feattn.rope_table(table, max_pos, 128, ROPE_THETA)
+    pos = torch.from_numpy(fill.positions).to(dev)
+    slots = torch.from_numpy(fill.slots).to(dev)
+    last_rows = torch.tensor([fill.qo[i + 1] - 1 for i in range(b.batch)], device=dev)
+    g = torch.Generator(device=dev).manual_seed(POOL_SEED)
+    shape = (b.blocks + 1, b.page, b.hkv, 128)
+    pools, q_dec = [], None
+    for _ in range(n):
+        kc = torch.zeros(shape, device=dev, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        q = torch.randn(rows, b.hq, 128, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(rows, b.hkv, 128, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(rows, b.hkv, 128, generator=g, device=dev).to(torch.bfloat16)
+        feattn.rope_append(q, k, v, kc, vc, pos, slots, table, rows, b.hq, b.hkv, 128, True, max_pos,
+                           b.cache_slots)
+        if q_dec is None:
+            q_dec = q[last_rows].contiguous()
+        del q, k, v
+        pools.append((kc, vc))
+    torch.cuda.synchronize()
+    return pools, q_dec
+
+
 def attn_setup(b, dev, dtype, causal, npools):
     import torch
 
@@ -109,16 +173,32 @@ def attn_setup(b, dev, dtype, causal, npools):
 
 
 def decode_headline(steps, warmup, dev):
+    """The headline step: one attention call over the decode batch, pools
+    rotated.  Returns the batch, the mean ms per step of the timed region
+    (value), the median over 10 further blocks of `steps` steps of each
+    block's mean, and the algorithmic bytes per step."""
     import torch
 
+    import feattn
     from feattn import workloads as W
 
     b = W.qwen3_8b_decode(seed=DECODE_SEED)
-    plan, step = attn_setup(b, dev, torch.bfloat16, True, 4)
+    plan = feattn.Plan(b.hq, b.hkv, 128, b.page, b.batch, b.max_pages(), True, b.blocks)
+    plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    pools, q = make_rope_pools(b, 4, dev)
+    out = torch.empty_like(q)
+    lse = torch.empty(b.rows, b.hq, device=dev)
+
+    def step(i):
+        kc, vc = pools[i % len(pools)]
+        plan.run(q, kc, vc, out, causal=True, lse=lse)
+
     ms = event_time_ms(step, steps, warmup)
+    per_step = event_block_means_ms(step, 10, steps)
     nbytes = W.decode_bytes(b)
     plan.close()
-    return b, ms, nbytes
+    del pools
+    return b, ms, statistics.median(per_step), nbytes
 
 
 def secondary(dev, only=None):
@@ -415,9 +495,10 @@ def main():
         print(json.dumps(secondary(dev, args.only)), flush=True)
         return
 
-    b, ms, nbytes = decode_headline(args.steps, args.warmup, dev)
+    b, ms, ms_med, nbytes = decode_headline(args.steps, args.warmup, dev)
     gbs = nbytes / ms / 1e6
-    log(f"decode: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+    log(f"decode: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak); "
+        f"median of 10 further blocks of {args.steps} steps: {ms_med * 1e3:.1f} us/step")
     sec = {} if args.no_secondary else secondary(dev)
     sec["copy_calibration"] = copy_calibration(dev)
     log("copy", sec["copy_calibration"])
@@ -430,7 +511,11 @@ def main():
         "data": "synthetic",
         "config": {"workload": "Qwen3-8B-shape paged decode attention: 64 seqs, ctx U[512,4096] "
                                "(seeded), hq 32 / hkv 8 / d 128, 16-token pages, bf16, 4 rotated "
-                               "KV pools",
+                               "KV pools; every context token's raw q/k/v ~ N(0,1), q and k rotated "
+                               "at the token's position (RoPE theta 1e6) and k/v written to its page "
+                               "slot by the fused RoPE + paged append; the decode rows are the last "
+                               "token's q",
+                   "rope_theta": ROPE_THETA,
                    "batch": b.batch, "context_tokens": sum(b.lens), "pages": b.blocks,
                    "seeds": {"lengths_and_pages": DECODE_SEED, "kv_pools": POOL_SEED, "q": Q_SEED}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
@@ -438,9 +523,14 @@ def main():
                      "traffic": measured_traffic(),
                      "algorithmic_bytes": nbytes,
                      "timed": "one fe_attn_run per step (attn_decode_kernel + attn_merge_kernel, "
-                              "the whole attention call), HIP events on the launch stream; traffic "
-                              "= DRAM read + write request counters of both kernels, "
-                              "profiles/decode_qwen3_8b_hbm_traffic.txt"},
+                              "the whole attention call), HIP events on the launch stream; "
+                              "achieved = algorithmic bytes / mean step time of the timed region; "
+                              "traffic = DRAM read + write request counters of both kernels, "
+                              "profiles/decode_qwen3_8b_hbm_traffic.txt",
+                     "ms_per_step_mean": round(ms, 5),
+                     "ms_per_step_median": round(ms_med, 5),
+                     "median_of": f"the mean step times of 10 further blocks of {args.steps} steps "
+                                  f"({10 * args.steps} launches) after the timed region"},
         "cpu_baseline": cpu,
         "secondary": sec,
     }

@@ -21,10 +21,19 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
 
 namespace {
 
-// 48 MiB: the whole split-KV budget of any plan with up to 190 query heads
-// (about 32.5 MiB at most) plus the work lists.  Each device the library
-// runs on holds its own copy until the process ends.
+// 48 MiB.  A plan's split-KV budget is max(1024, 64 MiB / (hq * 516 B))
+// partial slots of hq * 260 B each (fe_attn.cpp: partial_cap_for): at most
+// 32.25 MiB below 128 query heads and 1024 * hq * 260 B from 128 on, so the
+// full budget of any plan with up to 128 query heads (32.5 MiB) fits beside
+// 15.5 MiB of work lists and page table.  Each device the library runs on
+// holds its own copy from the time the library's code object is loaded
+// until the process ends, whether or not this entry point is called.
 constexpr size_t kScratchBytes = 48u << 20;
+constexpr size_t kFullBudgetHeads = 128;
+constexpr size_t kPartialSlotsFloor = 1024;
+constexpr size_t kPartialBytesPerHead = 128 * 2 + 4;  // 16-bit partial row + fp32 log2-LSE
+static_assert(kScratchBytes >= kPartialSlotsFloor * kFullBudgetHeads * kPartialBytesPerHead + (15u << 20),
+              "scratch must hold the split-KV budget of a 128-head plan plus 15 MiB of metadata");
 constexpr int kMaxDevices = 64;
 
 // Device address of each device's copy of `scratch`, looked up on the first

@@ -340,6 +340,16 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
                  void* out, float* lse, int causal, const int32_t* qo, const int32_t* kv, const int32_t* pages,
                  const int32_t* last, int batch, int rows, int hq, int hkv, int dim, int page, int blocks, int bf16,
                  hipStream_t st) {
+  // A capture would record the metadata copy below with a source in host
+  // memory that is released when this call returns: a replay would then
+  // read freed memory as work lists and page ids.  Refused before anything
+  // is enqueued.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t ce = hipStreamIsCapturing(st, &cap);
+  if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(FE_EINVAL, "attention (no-alloc): the stream is capturing a graph; capture the plan entry "
+                           "points (fe_attn_plan_prepare outside the capture, fe_attn_run inside) instead");
   if (batch < 0) return fail(FE_EINVAL, "batch must be non-negative");
   if (batch > 0 && kv == nullptr) return fail(FE_EINVAL, "null metadata pointer");
   // Capacity from the call itself: every sequence fits (the planner checks

@@ -114,6 +114,45 @@ def make_batch(hq: int, hkv: int, starts: Sequence[int], qlens: Sequence[int], s
     return build_metadata(b)
 
 
+def make_shared_prefix_batch(hq: int, hkv: int, groups, seed: int, page: int = PAGE,
+                             extra_pages: int = 0) -> Batch:
+    """Page tables that share pages across sequences, as a prefix-cache hit
+    produces them: BlockManager::probe (src/scheduler.cpp:6-17) hands every
+    sequence whose leading tokens match a published prefix the same page ids
+    for those whole pages, and the sequence's later pages come from the free
+    list (src/scheduler.cpp:31-33).  `groups` is a list of
+    (prefix_pages, [(start, qlen), ...]): each sequence of a group reuses the
+    group's prefix_pages page ids for its first prefix_pages * page tokens
+    and gets pages of its own for the rest.  Shared pages are never written
+    (src/scheduler.cpp:10), so start >= prefix_pages * page.  Page ids come
+    from one seeded permutation of the pool, shared prefixes first."""
+    import torch
+
+    seqs, own_need, pre_need = [], [], 0
+    for npre, members in groups:
+        pre_need += npre
+        for start, qlen in members:
+            if start < npre * page:
+                raise ValueError("a shared prefix page would be written")
+            seqs.append((start, qlen))
+            own_need.append(math.ceil((start + qlen) / page) - npre)
+    pool = pre_need + sum(own_need) + extra_pages
+    g = torch.Generator().manual_seed(seed * 7919 + 3)
+    perm = torch.randperm(pool, generator=g).tolist()
+    off, k, tables = pre_need, 0, []
+    pre_off = 0
+    for npre, members in groups:
+        prefix = perm[pre_off:pre_off + npre]
+        pre_off += npre
+        for _ in members:
+            tables.append(prefix + perm[off:off + own_need[k]])
+            off += own_need[k]
+            k += 1
+    b = Batch(hq=hq, hkv=hkv, page=page, blocks=pool, starts=[s for s, _ in seqs],
+              qlens=[q for _, q in seqs], tables=tables)
+    return build_metadata(b)
+
+
 def randn_bf16(shape, seed: int, dtype="bf16", device="cpu"):
     """N(0,1) fp32 from a seeded generator, rounded to bf16/fp16 (RNE)."""
     import torch

@@ -124,16 +124,23 @@ int fe_rope_append(void* q, const void* k, const void* v, void* k_cache,
  * blocks, bf16) prepared with (qo, kv, pages, last, batch, rows) and run
  * with (q, k_cache, v_cache, out, lse, causal): the same work lists, kernels
  * and bits.  The work lists and split-KV partials live in a 48 MiB device
- * array of the library (one per device, kept until the process ends); a
- * call that needs more returns FE_ECAPACITY.  Allocates no device or pinned
+ * array of the library (one per device, reserved when the library's code
+ * object loads on that device, whether or not this entry point is ever
+ * called, and kept until the process ends): enough for the full split-KV
+ * budget of any plan with up to 128 query heads plus 15.5 MiB of work lists
+ * and page table; a call that needs more returns FE_ECAPACITY.  Allocates no device or pinned
  * memory; the metadata goes to the device by one copy from pageable host
  * memory on `stream`, which HIP performs synchronously: the call returns
  * after the stream's earlier work and the copy have run.  For the same
- * reason the call must not be captured into a HIP graph (a
- * replay would copy from host memory the call has released; capture the
- * plan entry points instead).  Every call on a device shares that device's
- * array: calls that overlap on one device (other streams, other threads)
- * race, and calls ordered on one stream do not. */
+ * reason it cannot be captured into a HIP graph (a replay would copy from
+ * host memory the call has released): on a capturing stream it returns
+ * FE_EINVAL and enqueues nothing; capture the plan entry points instead.
+ * Every call on a device shares that device's array.  Calls ordered on one
+ * stream are safe.  Calls that overlap on one device (other streams, other
+ * threads) are not: a later call's copy overwrites the page table and work
+ * lists that an earlier call's kernels are still reading, so those kernels
+ * can read page ids of the other call, i.e. outside their own caches, and
+ * fault the device.  Order such calls on one stream or with events. */
 int fe_attn_run_noalloc(const void* q, const void* k_cache, const void* v_cache,
                         void* out, float* lse, int causal, const int32_t* qo,
                         const int32_t* kv, const int32_t* pages,

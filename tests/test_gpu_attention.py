@@ -173,6 +173,61 @@ def test_full_size_configs_sampled(dev, name, err_report):
     err_report(name, out[rows], lse[rows], want_out, want_lse)
     check(out[rows], lse[rows], want_out, want_lse)
     assert torch.isfinite(out.float()).all()
+    if ref_lib.available():
+        # the reference's own create_plan / prepare_plan / attention
+        # (src/portable_gpu_ops.cpp:18-44) on the same sampled sequences and
+        # the same device caches
+        ref = ref_lib.attention(sb, q[rows.to(dev)].contiguous(), kc, vc, causal).cpu()
+        err_report(name + "_ref", out[rows], None, ref, None)
+        torch.testing.assert_close(out[rows].float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+# Sequences sharing their leading pages, as prefix-cache hits leave them
+# (BlockManager::probe, src/scheduler.cpp:6-17; tests/host_tests.cpp:35-36):
+# (shared prefix pages, [(cached tokens, query rows), ...]) per group.
+SHARED = [
+    # decode rows and a 16-row block over one 3200-token prefix
+    (200, [(3205, 1), (3900, 1), (3200, 1), (3300, 16), (4500, 1)]),
+    # chunks over one 1024-token prefix (tile kernel), and a decode row
+    (64, [(1024, 100), (1061, 300), (2000, 1), (1024, 64)]),
+    # two 32K decode rows sharing 2000 pages: split-KV pieces read the same pages
+    (2000, [(32767, 1), (32767, 1)]),
+]
+
+
+def shared_prefix_batch(hq=32, hkv=8):
+    return W.make_shared_prefix_batch(hq, hkv, SHARED, seed=77, extra_pages=2)
+
+
+def test_shared_prefix_tables_share_pages():
+    """The generator's tables reuse page ids across sequences (the prefix)
+    and nowhere else; no sequence writes a shared page."""
+    b = shared_prefix_batch()
+    seen = {}
+    for s, t in enumerate(b.tables):
+        for i, p in enumerate(t):
+            seen.setdefault(p, []).append((s, i))
+    shared = {p: v for p, v in seen.items() if len(v) > 1}
+    assert len(shared) == 200 + 64 + 2000
+    assert all(len({i for _, i in v}) == 1 for v in shared.values())  # same position in every table
+    for s in range(b.batch):
+        for r in range(b.qo[s], b.qo[s + 1]):
+            assert b.slots[r] // 16 not in shared
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_shared_prefix_pages_vs_oracle(dev, causal, dtype):
+    """Decode, block, chunk and split-KV work over page tables that share
+    pages across sequences, against the oracle."""
+    b = shared_prefix_batch()
+    counts = feattn.describe(b.hq, b.hkv, 128, 16, b.batch, b.max_pages(), b.blocks, b.qo, b.kv,
+                             b.pages, b.last, b.batch, b.rows)
+    assert counts[0] > 0 and counts[1] > 0 and counts[2] > 0  # decode, tile and merged (split) rows
+    q, kc, vc = W.make_tensors(b, seed=78, dtype=dtype)
+    want_out, want_lse = A.run(b, q, kc, vc, causal)
+    out, lse = hip_attention(b, q, kc, vc, causal, dev)
+    check(out, lse, want_out, want_lse)
 
 
 def test_deterministic(dev):
@@ -258,6 +313,20 @@ def test_matches_reference_aten_on_device(dev, causal):
         ref = ref_lib.attention(b, q, kc, vc, causal).cpu()
         out, _ = hip_attention(b, q, kc, vc, causal, dev)
         torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.skipif(not ref_lib.available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_shared_prefix_pages_vs_reference_aten(dev, causal, dtype, err_report):
+    """Page tables sharing prefix pages through the reference's own ATen
+    attention (src/portable_gpu_ops.cpp:27-44) on the same device tensors."""
+    b = shared_prefix_batch()
+    q, kc, vc = W.make_tensors(b, seed=79, dtype=dtype, device=dev)
+    ref = ref_lib.attention(b, q, kc, vc, causal).cpu()
+    out, _ = hip_attention(b, q, kc, vc, causal, dev)
+    err_report(f"shared_{dtype}_{'c' if causal else 'nc'}_ref", out, None, ref, None)
+    torch.testing.assert_close(out.float(), ref.float(), atol=ATOL, rtol=RTOL)
 
 
 @pytest.mark.parametrize("seed", range(16))

@@ -13,6 +13,7 @@ import torch
 
 import feattn
 from feattn import workloads as W
+from test_gpu_known_counts import stream_cut_taken
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +50,43 @@ def test_noalloc_matches_plan_path_twice_second_smaller(dev):
     small = W.make_batch(16, 2, starts=[200, 64], qlens=[5, 1], seed=32, extra_pages=1)
     assert small.rows < big.rows and small.batch < big.batch
     both_paths(dev, small, False, "f16", 600)
+
+
+def test_noalloc_stream_cut_batch_small_then_big(dev):
+    """A batch planned by the equal cut of the tile stream (chunks split into
+    consecutive pieces with partial rows), run after a smaller call and
+    before one: the smaller call's metadata and partial rows are overwritten
+    by the bigger call's, and the next small call reads none of them."""
+    small = W.make_batch(16, 2, starts=[200, 64], qlens=[5, 1], seed=33, extra_pages=1)
+    both_paths(dev, small, True, "bf16", 700)
+    cut = W.make_batch(32, 8, starts=[6000, 9000, 300], qlens=[200, 64, 40], seed=45, extra_pages=1)
+    assert stream_cut_taken(cut, True) and stream_cut_taken(cut, False)
+    both_paths(dev, cut, True, "bf16", 710)
+    both_paths(dev, cut, False, "f16", 720)
+    both_paths(dev, small, False, "bf16", 730)
+
+
+def test_noalloc_refuses_a_capturing_stream(dev):
+    """Under stream capture the call returns FE_EINVAL before enqueuing
+    anything (its metadata copy would read released host memory on every
+    replay); the capture ends with an empty graph."""
+    b = W.make_batch(32, 8, starts=[100, 40], qlens=[1, 3], seed=9)
+    q = torch.zeros(b.rows, 32, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(b.blocks + 1, 16, 8, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.full_like(q, float("nan"))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="thread_local"):
+        with pytest.raises(RuntimeError, match="capturing"):
+            feattn.run_noalloc(q, kc, kc, out, b.qo, b.kv, b.pages, b.last, b.batch, b.rows, 32, 8, 128, 16,
+                               b.blocks, True)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+    # the stream is usable afterwards
+    feattn.run_noalloc(q, kc, kc, out, b.qo, b.kv, b.pages, b.last, b.batch, b.rows, 32, 8, 128, 16, b.blocks,
+                       True)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out.float()).any()
 
 
 def test_noalloc_rejects_calls_beyond_its_scratch(dev):
