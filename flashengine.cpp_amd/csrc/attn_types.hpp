@@ -13,7 +13,6 @@ namespace feattn {
 constexpr int kHeadDim = 128;  // the only head size the reference builds (flashinfer_attention.cu:23)
 constexpr int kTileTokens = 64;  // tokens per KV tile of the MFMA tile kernel (4 pages of 16)
 constexpr int kTileCols = 128;   // (q row, head) columns per tile work item (4 waves x 32)
-constexpr int kWideItemCols = 256;  // columns per item of the wide tile kernel (8 waves x 32)
 constexpr int kDecodeCols = 32;  // max (q row, head) columns of one decode work item (2 MFMA N blocks)
 constexpr int kDecodeWavesPerCu = 8;  // decode wavefronts resident per CU (one kv head each)
 

@@ -26,7 +26,6 @@ namespace feattn {
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st);
 int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
-hipError_t launch_wide(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
                        bool bf16, int max_pos, hipStream_t st);
@@ -212,12 +211,6 @@ struct Launch {
   bool bf16 = true;
   bool graph = false;
   int graph_tile = -1;  // graph plans: the first graph prepare had tile work (1) or not (0)
-  // Tile kernel of the lists just staged: the wide kernel (attn_wide.hip:
-  // 256-column items, one 8-wavefront workgroup per CU) when the planner
-  // chose it, else the tile kernel of attn_kernels.hip.  Graph plans keep
-  // the choice of their first graph prepare with tile work (-1: none yet).
-  int tile_wide = 0;
-  int graph_wide = -1;
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;         // wavefronts per decode workgroup
@@ -243,9 +236,6 @@ void record_lists(Launch& L, const BuiltPlan& bp, int nc) {
     L.n_tshare[m] = bp.mode[m].tile_off.empty() ? 0 : (int)bp.mode[m].tile_off.size() - 1;
     L.n_merge[m] = (int)bp.mode[m].merge.size();
   }
-  L.tile_wide = bp.tile_wide;
-  if (L.graph && L.graph_wide < 0 && (!bp.mode[0].tile.empty() || !bp.mode[1].tile.empty()))
-    L.graph_wide = bp.tile_wide;
 }
 
 // The work of a call runs on the device of its stream (the current device
@@ -312,11 +302,9 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
     t.items = reinterpret_cast<const WorkItem*>(L.dev + L.lay.tile[mode]);
     t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
     t.tile_off = reinterpret_cast<const int32_t*>(L.dev + L.lay.tshare[mode]);
-    const bool wide = L.tile_wide != 0;
-    const int grid = L.graph ? (wide ? L.sh.num_cus : L.grid_tile_cap) : L.n_tshare[mode];
-    e = wide ? launch_wide(t, L.bf16, causal != 0, std::max(grid, 1), st)
-             : launch_tile(t, L.bf16, causal != 0, std::max(grid, 1), st);
-    if (e != hipSuccess) return hip_fail(e, wide ? "wide tile kernel launch" : "tile kernel launch");
+    const int grid = L.graph ? L.grid_tile_cap : L.n_tshare[mode];
+    e = launch_tile(t, L.bf16, causal != 0, std::max(grid, 1), st);
+    if (e != hipSuccess) return hip_fail(e, "tile kernel launch");
   }
   if (L.graph || L.n_merge[mode] > 0) {
     MergeArgs m{};
@@ -507,9 +495,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   std::string err;
   int rc = check_stream_device(static_cast<hipStream_t>(stream), p->device);
   if (rc != FE_OK) return rc;
-  PlanShape psh = L.sh;
-  if (graph && L.graph_wide >= 0) psh.wide = L.graph_wide;  // the captured tile kernel
-  rc = build_plan(psh, qo, kv, pages, last, batch, rows, bp, err);
+  rc = build_plan(L.sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   int nc = bp.decode_nc;
   int graph_nc = p->graph_nc, graph_tile = L.graph_tile;

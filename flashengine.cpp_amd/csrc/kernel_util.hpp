@@ -53,25 +53,6 @@ __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) 
       : "memory");
 }
 
-// One dword per active lane, lane i landing at LDS lds_addr + 4 i (run with
-// one active lane to fetch a single word).
-__device__ __forceinline__ void lds_dma4(const void* gaddr, uint32_t lds_addr) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dword %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(gaddr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))  // wave-uniform by construction
-      : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_read4(uint32_t lds_addr) {
-  typedef __attribute__((address_space(3))) uint32_t lds_u32;
-  return *(lds_u32*)(uintptr_t)lds_addr;
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

@@ -99,8 +99,8 @@ namespace {
 // as in the longest-first list.  Returns false, leaving `ml` alone, when the
 // cut needs more partial slots or items than `slot_budget` / `item_cap`.
 bool cut_tile_stream(const std::vector<SeqInfo>& seqs, int G, int hkv, bool causal, int slots, int partial_base,
-                     int slot_budget, int item_cap, int item_cols, ModeLists& ml) {
-  const int qr = item_cols / G;
+                     int slot_budget, int item_cap, ModeLists& ml) {
+  const int qr = kTileCols / G;
   const int n_shares = slots / hkv;
   if (n_shares < 1) return false;
   struct Chunk {
@@ -115,7 +115,7 @@ bool cut_tile_stream(const std::vector<SeqInfo>& seqs, int G, int hkv, bool caus
       const int nq = std::min(qr, s.qlen - i0);
       const int extent = causal ? std::min(s.len, s.len - s.qlen + i0 + nq) : s.len;
       const int tiles = ceil_div(extent, kTileTokens);
-      const int c = nq * G > item_cols / 2 ? 2 : 1;
+      const int c = nq * G > kTileCols / 2 ? 2 : 1;
       ch.push_back(Chunk{b, s.qo + i0, nq, extent, tiles, c});
       total += (int64_t)tiles * c;
     }
@@ -393,14 +393,7 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
   }
 
   // ---- tile items, per mask mode.
-  bool wide = sh.wide > 0;
-  if (sh.wide < 0)
-    for (int b = 0; b < batch && !wide; ++b)
-      wide = out.seqs[b].qlen * G > kDecodeCols && out.seqs[b].qlen * G > kTileCols / 2;
-  out.tile_wide = wide ? 1 : 0;
-  const int item_cols = wide ? kWideItemCols : kTileCols;
-  const int tslots = wide ? sh.num_cus : sh.tile_slots;  // one wide workgroup per CU, else two
-  const int qr = item_cols / G;  // query rows per tile item
+  const int qr = kTileCols / G;  // query rows per tile item
   for (int causal = 0; causal < 2; ++causal) {
     ModeLists& ml = out.mode[causal];
     ml.partial_rows = out.decode_partials;
@@ -411,9 +404,9 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
       if (s.qlen * G > kDecodeCols) pairs += (int64_t)ceil_div(s.qlen, qr) * sh.hkv;
     }
     if (pairs == 0) continue;
-    // Aim for about 4 items per resident workgroup (2 per CU, or 1 wide),
-    // several rounds in longest-first order; never split below 256 tokens.
-    int want = (int)std::max<int64_t>(1, ((int64_t)tslots * 4 + pairs - 1) / pairs);
+    // Aim for about 8 items per compute unit (2 resident workgroups, several
+    // rounds in longest-first order); never split below 256 tokens.
+    int want = (int)std::max<int64_t>(1, ((int64_t)sh.num_cus * 8 + pairs - 1) / pairs);
     for (;;) {
       ml.tile.clear();
       ml.tile.reserve((size_t)std::min<int64_t>(pairs * want, sh.item_cap + 1));  // at most want pieces per pair
@@ -437,9 +430,9 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
           for (int sp = 0; sp < ns; ++sp) {
             const int t0 = sp * chunk;
             const int t1 = std::min(extent, t0 + chunk);
-            // Cost ~ tiles times the column blocks each wavefront computes
-            // (1 for items of at most half the item width, else 2).
-            const int cost = ceil_div(t1 - t0, kTileTokens) * (nq * G > item_cols / 2 ? 2 : 1);
+            // Cost ~ tiles times the 16-column blocks each wavefront
+            // computes (1 for items of <= 64 columns, else 2).
+            const int cost = ceil_div(t1 - t0, kTileTokens) * (nq * G > kTileCols / 2 ? 2 : 1);
             for (int h = 0; h < sh.hkv; ++h)
               ml.tile.push_back(WorkItem{b, s.qo + i0, nq, h, t0, t1, base < 0 ? -1 : base + sp * nq, cost});
           }
@@ -452,14 +445,14 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
       }
       want = std::max(1, want / 2);
     }
-    assign_shares(ml.tile, tslots, ml.tile_off);
+    assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
     // When the longest-first list had to split chunks anyway, an equal cut
     // of the tile stream balances the workgroups to within a tile, usually
     // with fewer pieces; it replaces the list if it needs no more partial rows.
     if (ml.partial_rows > out.decode_partials) {
       ModeLists cut;
-      if (cut_tile_stream(out.seqs, G, sh.hkv, causal != 0, tslots, out.decode_partials, slot_budget,
-                          sh.item_cap, item_cols, cut) &&
+      if (cut_tile_stream(out.seqs, G, sh.hkv, causal != 0, sh.tile_slots, out.decode_partials, slot_budget,
+                          sh.item_cap, cut) &&
           cut.partial_rows <= ml.partial_rows)
         ml = std::move(cut);
     }

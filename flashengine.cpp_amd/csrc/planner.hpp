@@ -24,11 +24,6 @@ struct PlanShape {
   int tile_slots = 512;     // workgroups of one tile launch (two resident per CU)
   int item_cap = 1 << 16;   // work items per list
   int partial_cap = 4096;   // split-KV partial slots ([hq][128] fp32 each)
-  // Tile kernel: -1 chooses (the wide kernel when some tile sequence has more
-  // than 64 (query row, head) columns), 0 / 1 force the 128-column tile
-  // kernel / the 256-column wide kernel (graph plans keep their first
-  // choice).
-  int wide = -1;
 };
 
 struct ModeLists {
@@ -47,8 +42,6 @@ struct BuiltPlan {
   int decode_partials = 0;
   std::vector<MergeRow> decode_merge;
   int decode_nc = 16;            // 16 or 32 columns per decode item (MFMA column blocks x 16)
-  int tile_wide = 0;             // tile items of up to 256 columns for the wide kernel (one
-                                 // workgroup per CU), else up to 128 for the tile kernel
   ModeLists mode[2];             // [0] full (non-causal), [1] causal
 };
 

@@ -13,21 +13,6 @@ def plan_args(b, max_pages=None, max_batch=None):
             b.blocks, b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
 
 
-def wide_plan(b):
-    """The planner's tile-kernel choice: 256-column items (the wide kernel,
-    one workgroup per CU) when some tile sequence has more than 64
-    (row, head) columns, else 128-column items over two workgroups per CU."""
-    return any(q * b.group > 64 for q in b.qlens)
-
-
-def item_cols(b):
-    return 256 if wide_plan(b) else 128
-
-
-def tile_shares(b):
-    return 256 if wide_plan(b) else 512
-
-
 def coverage(b, causal):
     """Counts, per (row, kv head, token), how often a work item covers it
     where the token is visible to the row."""
@@ -43,7 +28,7 @@ def coverage(b, causal):
         assert t0 % 16 == 0
         if kind == 1:
             assert t0 % 64 == 0
-            assert nq * b.group <= item_cols(b)
+            assert nq * b.group <= 128
         else:
             assert nq * b.group <= 32  # at most two 16-column MFMA blocks
         for r in range(q0, q0 + nq):
@@ -132,9 +117,9 @@ def test_tile_stream_cut_balances_chunks(hq, hkv, causal):
         else:
             runs.append((it[4], [it]))
     assert [h for h, _ in runs] == list(range(hkv)) * (len(runs) // hkv)
-    cost = lambda x: ((x[6] - x[5] + 63) // 64) * (2 if x[3] * b.group > item_cols(b) // 2 else 1)
+    cost = lambda x: ((x[6] - x[5] + 63) // 64) * (2 if x[3] * b.group > 64 else 1)
     loads = [sum(cost(x) for x in runs[k][1]) for k in range(0, len(runs), hkv)]
-    shares = tile_shares(b) // hkv
+    shares = 512 // hkv
     assert len(loads) <= shares
     assert max(loads) <= -(-sum(loads) // shares) + 1
 
