@@ -136,6 +136,8 @@ def _check(rc: int) -> None:
 
 
 def _i32(values: Sequence[int]):
+    if isinstance(values, ctypes.Array) and values._type_ is ctypes.c_int32:
+        return values  # already converted (callers that prepare every step convert once)
     arr = (ctypes.c_int32 * max(1, len(values)))(*values)
     return arr
 
