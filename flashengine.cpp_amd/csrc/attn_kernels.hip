@@ -720,14 +720,18 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
   const int hq = a.hq;
   const int hpairs = (hq + 1) >> 1;
   const int stride = gridDim.x * 4;
-  int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6);
-  // The first row record is requested together with the row count (its
-  // index is clamped into the buffer; it is used only below the count).
-  MergeRow mr = a.rows[min(pair / hpairs, a.rows_cap - 1)];
-  const int n_pairs = uniform(*a.n_rows) * hpairs;
+  // A graph launch folds the list of the latest prepare, found through the
+  // header; an eager launch is handed the list and its length.
+  const MergeRow* rows = a.rows;
+  int n_rows = a.n_rows;
+  if (a.count_base != nullptr) {
+    n_rows = uniform(a.count_base[0]);
+    rows += uniform(a.count_base[1]);
+  }
+  const int n_pairs = n_rows * hpairs;
   const int d = 4 * (lane & 31);
-  for (; pair < n_pairs; pair += stride) {
-    if (pair >= stride) mr = a.rows[pair / hpairs];
+  for (int pair = blockIdx.x * 4 + uniform(threadIdx.x >> 6); pair < n_pairs; pair += stride) {
+    const MergeRow mr = rows[pair / hpairs];
     const int h = 2 * (pair % hpairs) + (lane >> 5);
     const bool on = h < hq;
     const int hh = on ? h : hq - 1;

@@ -91,8 +91,8 @@ struct AttnArgs {
   const SeqInfo* seqs;
   const int32_t* pages;
   const WorkItem* items;
-  const int32_t* n_items;  // device-resident count (graph replays read the current one)
-  const int32_t* tile_off;   // tile only: items of workgroup b = [tile_off[b], tile_off[b+1])
+  const int32_t* n_items;  // tile only, device-resident: end of the item list (graph replays read the current one)
+  const int32_t* tile_off;   // tile only: items of workgroup b = [tile_off[b], min(tile_off[b+1], *n_items))
   const DecodeItem* ditems;  // decode only: the pieces, share by share
   const ShareStart* shares;  // decode only: one record per share
   int n_share_cap;           // decode only: records in `shares`
@@ -108,9 +108,9 @@ struct AttnArgs {
 struct MergeArgs {
   uint16_t* out;
   float* lse;
-  const MergeRow* rows;
-  const int32_t* n_rows;
-  int rows_cap;            // entries of `rows`
+  const MergeRow* rows;       // the records (eager launches) or the list they are indexed from (graph launches)
+  int n_rows;                 // eager launches: records at `rows`
+  const int32_t* count_base;  // graph launches, device-resident: records to fold, index of the first in `rows`
   const uint16_t* part_o;
   const float* part_lse;
   int hq;

@@ -4,8 +4,8 @@
 // counts) plus the split-KV partial buffers, all allocated once at create
 // time from the capacity arguments, like the reference's FlashInfer plan
 // (src/flashinfer_attention.cu:14-27).  prepare() builds the work lists on
-// the host into a pinned mirror of the arena and copies the used ranges on
-// the caller's stream; run() only launches kernels, whose grids depend on
+// the host into a pinned mirror of the arena and stages them with one copy
+// on the caller's stream; run() only launches kernels, whose grids depend on
 // the plan capacity in graph mode, so a captured graph stays valid across
 // prepares.
 #include "fe_attn.h"
@@ -74,63 +74,102 @@ int partial_cap_for(int hq) {
   return hq > 0 ? (int)std::max<size_t>(1024, kPartialBytes / ((size_t)hq * (kHeadDim + 1) * sizeof(float))) : 1024;
 }
 
-// Records held by each region of a metadata arena.  A plan sizes them from
-// its capacity; the one-shot entry from the lists of the call itself (a mode
-// whose tshare region is empty is not staged).
+// A metadata arena is
+//   [header | seqs | tshare[0] | tshare[1] | shares | heap ......]
+// The first five regions have fixed sizes.  The heap holds the lists whose
+// lengths vary from prepare to prepare (page table, decode pieces, tile
+// items and merge records of both masks), packed one after another; every
+// index a kernel follows into them (a share's item range, page_off, tile
+// offsets, the header's tile ends and merge bases) is stored relative to
+// the heap start.  So one prepare stages the arena with a single copy of
+// [0, end of the heap's used part) (each small host-to-device copy costs
+// several microseconds on the stream), and the region pointers of a
+// captured launch stay valid.
+//
+// Record counts of the fixed regions and bytes of the heap.  A plan sizes
+// them from its capacity, the one-shot entry from the call's own lists (a
+// mode with no tshare records is not staged).
 struct Regions {
-  size_t seqs, pages, shares, decode, tile[2], tshare[2], merge[2];
+  size_t seqs, tshare[2], shares, heap;
 };
 
-// Offsets of the regions inside a metadata arena (same layout on host and device).
 struct Layout {
   Regions n;
-  size_t seqs, pages, counts, dshare, decode, tile[2], tshare[2], merge[2], total;
+  size_t header, seqs, tshare[2], shares, heap, total;  // byte offsets
 };
 
 Layout make_layout(const Regions& r) {
   Layout l;
   l.n = r;
   size_t off = 0;
+  l.header = off;
+  off = align256(off + sizeof(int32_t) * 16);
   l.seqs = off;
   off = align256(off + sizeof(SeqInfo) * r.seqs);
-  l.pages = off;
-  off = align256(off + sizeof(int32_t) * r.pages);
-  l.counts = off;
-  off = align256(off + sizeof(int32_t) * 8);
-  l.dshare = off;
-  off = align256(off + sizeof(ShareStart) * r.shares);
-  l.decode = off;
-  off = align256(off + sizeof(DecodeItem) * r.decode);
   for (int m = 0; m < 2; ++m) {
-    l.tile[m] = off;
-    off = align256(off + sizeof(WorkItem) * r.tile[m]);
     l.tshare[m] = off;
     off = align256(off + sizeof(int32_t) * r.tshare[m]);
   }
-  for (int m = 0; m < 2; ++m) {
-    l.merge[m] = off;
-    off = align256(off + sizeof(MergeRow) * r.merge[m]);
-  }
+  l.shares = off;
+  off = align256(off + sizeof(ShareStart) * r.shares);
+  l.heap = off;
+  off = align256(off + r.heap);
   l.total = off;
   return l;
+}
+
+// Byte offsets of the lists inside the heap (each 256-byte aligned, so a
+// list's first record index is its offset over the record size).
+struct HeapPlace {
+  size_t pages, decode, tile[2], merge[2], used;
+};
+
+HeapPlace place_heap(size_t pages, size_t decode, const size_t tile[2], const size_t merge[2]) {
+  HeapPlace p;
+  size_t off = 0;
+  auto put = [&](size_t bytes) {
+    const size_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  p.pages = put(sizeof(int32_t) * pages);
+  p.decode = put(sizeof(DecodeItem) * decode);
+  for (int m = 0; m < 2; ++m) p.tile[m] = put(sizeof(WorkItem) * tile[m]);
+  for (int m = 0; m < 2; ++m) p.merge[m] = put(sizeof(MergeRow) * merge[m]);
+  p.used = off;
+  return p;
+}
+
+// Places the lists of `bp` for the staged mask modes.
+HeapPlace place_lists(const BuiltPlan& bp, int npages, const bool staged[2]) {
+  size_t tile[2], merge[2];
+  for (int m = 0; m < 2; ++m) {
+    tile[m] = staged[m] ? bp.mode[m].tile.size() : 0;
+    merge[m] = staged[m] ? bp.mode[m].merge.size() : 0;
+  }
+  return place_heap((size_t)npages, bp.decode_items.size(), tile, merge);
 }
 
 Regions capacity_regions(const PlanShape& sh) {
   Regions r;
   r.seqs = (size_t)sh.max_batch;
-  r.pages = (size_t)sh.max_batch * sh.max_pages;
   r.shares = (size_t)share_cap(sh);
-  r.decode = (size_t)sh.item_cap;
-  for (int m = 0; m < 2; ++m) {
-    r.tile[m] = (size_t)sh.item_cap;
-    r.tshare[m] = (size_t)sh.tile_slots + 1;
-    r.merge[m] = (size_t)sh.partial_cap;
-  }
+  const size_t tile[2] = {(size_t)sh.item_cap, (size_t)sh.item_cap};
+  const size_t merge[2] = {(size_t)sh.partial_cap, (size_t)sh.partial_cap};
+  for (int m = 0; m < 2; ++m) r.tshare[m] = (size_t)sh.tile_slots + 1;
+  r.heap = place_heap((size_t)sh.max_batch * sh.max_pages, (size_t)sh.item_cap, tile, merge).used;
   return r;
 }
 
-// counts[] indices
-enum { kCntDecode = 0, kCntTile0 = 1, kCntTile1 = 2, kCntMerge0 = 3, kCntMerge1 = 4 };
+// header[] indices.  Tile ends are heap indices (a workgroup's items end at
+// min(tile_off[b + 1], end)); each merge count is followed by its base.
+enum {
+  kHdrDecodeShares = 0,
+  kHdrTileEnd0 = 2,
+  kHdrTileEnd1 = 3,
+  kHdrMerge0 = 4,  // count, base
+  kHdrMerge1 = 6,  // count, base
+};
 
 // Validated shape (host-only sizes).
 int make_shape(int hq, int hkv, int dim, int page, int max_batch, int max_pages, int blocks, PlanShape& sh,
@@ -161,32 +200,65 @@ int device_sizes(PlanShape& sh, int device, std::string& err) {
   return FE_OK;
 }
 
-// Writes the lists of `bp` into the host image `h` of the arena layout `l`.
-int write_image(uint8_t* h, const Layout& l, const PlanShape& sh, const BuiltPlan& bp, const int32_t* pages,
-                int npages, std::string& err) {
+// Writes the lists of `bp` into the host image `h` of the arena layout `l`,
+// the heap lists at `hp`, every heap index shifted by its list's start.
+// Returns the bytes to copy (the image up to the end of the heap's used
+// part) in `bytes`.
+int write_image(uint8_t* h, const Layout& l, const HeapPlace& hp, const PlanShape& sh, const BuiltPlan& bp,
+                const int32_t* pages, int npages, size_t& bytes, std::string& err) {
   const int n_shares = (int)bp.decode_starts.size();
   const int scap = (int)l.n.shares;
   if (n_shares > scap) {
     err = "attention metadata exceeds capacity: decode shares";
     return FE_ECAPACITY;
   }
-  std::memcpy(h + l.seqs, bp.seqs.data(), sizeof(SeqInfo) * bp.seqs.size());
-  if (npages > 0) std::memcpy(h + l.pages, pages, sizeof(int32_t) * npages);
-  int32_t* cnt = reinterpret_cast<int32_t*>(h + l.counts);
-  std::memset(cnt, 0, sizeof(int32_t) * 8);
-  cnt[kCntDecode] = n_shares;
-  // Every record up to the capacity is written: a graph launch covers them
-  // all, and records past the shares in use must read as empty.
-  std::memcpy(h + l.dshare, bp.decode_starts.data(), sizeof(ShareStart) * n_shares);
-  std::memset(h + l.dshare + sizeof(ShareStart) * n_shares, 0, sizeof(ShareStart) * (size_t)(scap - n_shares));
-  std::memcpy(h + l.decode, bp.decode_items.data(), sizeof(DecodeItem) * bp.decode_items.size());
+  if (bp.seqs.size() > l.n.seqs || hp.used > l.n.heap) {
+    err = "attention metadata exceeds capacity: work lists";
+    return FE_ECAPACITY;
+  }
+  uint8_t* heap = h + l.heap;
+  const int32_t pages_base = (int32_t)(hp.pages / sizeof(int32_t));
+  const int32_t decode_base = (int32_t)(hp.decode / sizeof(DecodeItem));
+
+  int32_t* hdr = reinterpret_cast<int32_t*>(h + l.header);
+  std::memset(hdr, 0, sizeof(int32_t) * 16);
+  hdr[kHdrDecodeShares] = n_shares;
+
+  SeqInfo* seqs = reinterpret_cast<SeqInfo*>(h + l.seqs);
+  for (size_t b = 0; b < bp.seqs.size(); ++b) {
+    seqs[b] = bp.seqs[b];
+    seqs[b].page_off += pages_base;
+  }
+  if (npages > 0) std::memcpy(heap + hp.pages, pages, sizeof(int32_t) * npages);
+
+  auto shift_piece = [&](DecodeItem d) {
+    d.page_off += pages_base;
+    return d;
+  };
+  DecodeItem* items = reinterpret_cast<DecodeItem*>(heap + hp.decode);
+  for (size_t i = 0; i < bp.decode_items.size(); ++i) items[i] = shift_piece(bp.decode_items[i]);
+  // Every share record up to the capacity is written: a graph launch covers
+  // them all, and records past the shares in use must read as empty.
+  ShareStart* ss = reinterpret_cast<ShareStart*>(h + l.shares);
+  for (int k = 0; k < n_shares; ++k) {
+    ss[k] = bp.decode_starts[k];
+    ss[k].it_begin += decode_base;
+    ss[k].it_end += decode_base;
+    ss[k].first = shift_piece(ss[k].first);
+  }
+  std::memset(ss + n_shares, 0, sizeof(ShareStart) * (size_t)(scap - n_shares));
+
   const int tslots = sh.tile_slots;
   for (int m = 0; m < 2; ++m) {
     if (l.n.tshare[m] == 0) continue;  // mode not staged
-    cnt[m ? kCntTile1 : kCntTile0] = (int32_t)bp.mode[m].tile.size();
-    cnt[m ? kCntMerge1 : kCntMerge0] = (int32_t)bp.mode[m].merge.size();
-    std::memcpy(h + l.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * bp.mode[m].tile.size());
-    std::memcpy(h + l.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * bp.mode[m].merge.size());
+    const int32_t tile_base = (int32_t)(hp.tile[m] / sizeof(WorkItem));
+    const int32_t n_tile = (int32_t)bp.mode[m].tile.size();
+    const size_t n_merge = bp.mode[m].merge.size();
+    hdr[m ? kHdrTileEnd1 : kHdrTileEnd0] = tile_base + n_tile;
+    hdr[(m ? kHdrMerge1 : kHdrMerge0) + 0] = (int32_t)n_merge;
+    hdr[(m ? kHdrMerge1 : kHdrMerge0) + 1] = (int32_t)(hp.merge[m] / sizeof(MergeRow));
+    if (n_tile > 0) std::memcpy(heap + hp.tile[m], bp.mode[m].tile.data(), sizeof(WorkItem) * n_tile);
+    if (n_merge > 0) std::memcpy(heap + hp.merge[m], bp.mode[m].merge.data(), sizeof(MergeRow) * n_merge);
     // share offsets up to the launch capacity: shares past those in use are
     // empty (a graph launch covers every slot)
     const std::vector<int32_t>& off = bp.mode[m].tile_off;
@@ -196,8 +268,9 @@ int write_image(uint8_t* h, const Layout& l, const PlanShape& sh, const BuiltPla
       return FE_ECAPACITY;
     }
     int32_t* dst = reinterpret_cast<int32_t*>(h + l.tshare[m]);
-    for (int k = 0; k <= tslots; ++k) dst[k] = k <= used && !off.empty() ? off[k] : (int32_t)bp.mode[m].tile.size();
+    for (int k = 0; k <= tslots; ++k) dst[k] = tile_base + (k <= used && !off.empty() ? off[k] : n_tile);
   }
+  bytes = l.heap + hp.used;
   return FE_OK;
 }
 
@@ -212,6 +285,7 @@ struct Launch {
   bool graph = false;
   int graph_tile = -1;  // graph plans: the first graph prepare had tile work (1) or not (0)
   int n_decode = 0, n_tile[2] = {0, 0}, n_merge[2] = {0, 0};
+  size_t merge_off[2] = {0, 0};  // heap offsets of the merge lists just staged
   int n_tshare[2] = {0, 0};  // tile shares (workgroups) in use per mask mode
   int decode_wg = 8;         // wavefronts per decode workgroup
   int decode_nc = 16;
@@ -228,8 +302,9 @@ void init_launch(Launch& L, const PlanShape& sh, bool bf16) {
 }
 
 // Launch sizes of the lists just staged.
-void record_lists(Launch& L, const BuiltPlan& bp, int nc) {
+void record_lists(Launch& L, const BuiltPlan& bp, const HeapPlace& hp, int nc) {
   L.decode_nc = nc;
+  for (int m = 0; m < 2; ++m) L.merge_off[m] = hp.merge[m];
   L.n_decode = (int)bp.decode_starts.size() * L.sh.hkv;  // busy decode wavefronts
   for (int m = 0; m < 2; ++m) {
     L.n_tile[m] = (int)bp.mode[m].tile.size();
@@ -267,7 +342,8 @@ int check_tensors(const void* q, const void* k_cache, const void* v_cache, const
 int launch_all(const Launch& L, const void* q, const void* k_cache, const void* v_cache, void* out, float* lse,
                int causal, hipStream_t st) {
   const int mode = causal ? 1 : 0;
-  const int32_t* counts = reinterpret_cast<const int32_t*>(L.dev + L.lay.counts);
+  const int32_t* hdr = reinterpret_cast<const int32_t*>(L.dev + L.lay.header);
+  const uint8_t* heap = L.dev + L.lay.heap;
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.kc = static_cast<const uint16_t*>(k_cache);
@@ -275,7 +351,7 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
   a.out = static_cast<uint16_t*>(out);
   a.lse = lse;
   a.seqs = reinterpret_cast<const SeqInfo*>(L.dev + L.lay.seqs);
-  a.pages = reinterpret_cast<const int32_t*>(L.dev + L.lay.pages);
+  a.pages = reinterpret_cast<const int32_t*>(heap);
   a.part_o = L.part_o;
   a.part_lse = L.part_lse;
   a.hq = L.sh.hq;
@@ -288,10 +364,9 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
   hipError_t e;
   if (L.graph || L.n_decode > 0) {
     AttnArgs d = a;
-    d.ditems = reinterpret_cast<const DecodeItem*>(L.dev + L.lay.decode);
-    d.shares = reinterpret_cast<const ShareStart*>(L.dev + L.lay.dshare);
+    d.ditems = reinterpret_cast<const DecodeItem*>(heap);
+    d.shares = reinterpret_cast<const ShareStart*>(L.dev + L.lay.shares);
     d.n_share_cap = (int)L.lay.n.shares;
-    d.n_items = counts + kCntDecode;
     const int wv = L.decode_wg;
     const int grid = L.graph ? L.grid_decode_cap : std::min(L.grid_decode_cap, (L.n_decode + wv - 1) / wv);
     e = launch_decode(d, L.bf16, L.decode_wg, L.decode_nc / 16, causal ? 1 : 0, std::max(grid, 1), st);
@@ -299,8 +374,8 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
   }
   if (L.graph ? L.graph_tile > 0 : L.n_tile[mode] > 0) {
     AttnArgs t = a;
-    t.items = reinterpret_cast<const WorkItem*>(L.dev + L.lay.tile[mode]);
-    t.n_items = counts + (mode ? kCntTile1 : kCntTile0);
+    t.items = reinterpret_cast<const WorkItem*>(heap);
+    t.n_items = hdr + (mode ? kHdrTileEnd1 : kHdrTileEnd0);
     t.tile_off = reinterpret_cast<const int32_t*>(L.dev + L.lay.tshare[mode]);
     const int grid = L.graph ? L.grid_tile_cap : L.n_tshare[mode];
     e = launch_tile(t, L.bf16, causal != 0, std::max(grid, 1), st);
@@ -310,9 +385,13 @@ int launch_all(const Launch& L, const void* q, const void* k_cache, const void* 
     MergeArgs m{};
     m.out = static_cast<uint16_t*>(out);
     m.lse = lse;
-    m.rows = reinterpret_cast<const MergeRow*>(L.dev + L.lay.merge[mode]);
-    m.n_rows = counts + (mode ? kCntMerge1 : kCntMerge0);
-    m.rows_cap = (int)std::max<size_t>(1, L.lay.n.merge[mode]);
+    if (L.graph) {
+      m.rows = reinterpret_cast<const MergeRow*>(heap);
+      m.count_base = hdr + (mode ? kHdrMerge1 : kHdrMerge0);
+    } else {
+      m.rows = reinterpret_cast<const MergeRow*>(heap + L.merge_off[mode]);
+      m.n_rows = L.n_merge[mode];
+    }
     m.part_o = L.part_o;
     m.part_lse = L.part_lse;
     m.hq = L.sh.hq;
@@ -374,14 +453,13 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
   if (rc != FE_OK) return fail(rc, err);
   const int mode = causal ? 1 : 0;
   const int npages = batch > 0 ? kv[batch] : 0;
+  const bool staged[2] = {mode == 0, mode == 1};
+  const HeapPlace hp = place_lists(bp, npages, staged);
   Regions r{};
   r.seqs = bp.seqs.size();
-  r.pages = (size_t)npages;
-  r.shares = (size_t)share_cap(sh);
-  r.decode = bp.decode_items.size();
-  r.tile[mode] = bp.mode[mode].tile.size();
   r.tshare[mode] = (size_t)sh.tile_slots + 1;
-  r.merge[mode] = bp.mode[mode].merge.size();
+  r.shares = (size_t)share_cap(sh);
+  r.heap = hp.used;
   Launch L;
   init_launch(L, sh, bf16 != 0);
   L.lay = make_layout(r);
@@ -394,20 +472,21 @@ int attn_oneshot(uint8_t* arena, size_t bytes, int device, const void* q, const 
                                   " bytes of device scratch, more than the " + std::to_string(bytes) + " it holds");
   // Nothing in the arena has to start at zero, whatever an earlier call
   // left there: the copy below writes every metadata field the kernels read
-  // (counts, share records, lists), and every partial slot a merge reads is
+  // (header, share records, lists), and every partial slot a merge reads is
   // written by this call's decode or tile kernel first.
   std::vector<uint8_t> image(L.lay.total);
-  rc = write_image(image.data(), L.lay, sh, bp, pages, npages, err);
+  size_t stage_bytes = 0;
+  rc = write_image(image.data(), L.lay, hp, sh, bp, pages, npages, stage_bytes, err);
   if (rc != FE_OK) return fail(rc, err);
   // The image is pageable host memory, which HIP copies synchronously (the
   // call returns once the copy has run on `st`), so it may be released right
   // after.
-  hipError_t e = hipMemcpyAsync(arena, image.data(), L.lay.total, hipMemcpyHostToDevice, st);
+  hipError_t e = hipMemcpyAsync(arena, image.data(), stage_bytes, hipMemcpyHostToDevice, st);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(attention metadata)");
   L.dev = arena;
   L.part_o = reinterpret_cast<uint16_t*>(arena + o_off);
   L.part_lse = reinterpret_cast<float*>(arena + lse_off);
-  record_lists(L, bp, bp.decode_nc);
+  record_lists(L, bp, hp, bp.decode_nc);
   return launch_all(L, q, k_cache, v_cache, out, lse, causal, st);
 }
 }  // namespace feattn
@@ -527,22 +606,12 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   const Layout& l = L.lay;
   uint8_t* h = p->host;
   const int npages = batch > 0 ? kv[batch] : 0;
-  if (write_image(h, l, L.sh, bp, pages, npages, err) != FE_OK) return fail(FE_ECAPACITY, err);
-  auto copy = [&](size_t off, size_t bytes) -> hipError_t {
-    if (bytes == 0) return hipSuccess;
-    return hipMemcpyAsync(p->dev + off, h + off, bytes, hipMemcpyHostToDevice, st);
-  };
-  hipError_t e = hipSuccess;
-  if (e == hipSuccess) e = copy(l.seqs, sizeof(SeqInfo) * bp.seqs.size());
-  if (e == hipSuccess) e = copy(l.pages, sizeof(int32_t) * npages);
-  if (e == hipSuccess) e = copy(l.counts, sizeof(int32_t) * 8);
-  if (e == hipSuccess) e = copy(l.dshare, sizeof(ShareStart) * l.n.shares);
-  if (e == hipSuccess) e = copy(l.decode, sizeof(DecodeItem) * bp.decode_items.size());
-  for (int m = 0; m < 2 && e == hipSuccess; ++m) {
-    e = copy(l.tile[m], sizeof(WorkItem) * bp.mode[m].tile.size());
-    if (e == hipSuccess) e = copy(l.tshare[m], sizeof(int32_t) * l.n.tshare[m]);
-    if (e == hipSuccess) e = copy(l.merge[m], sizeof(MergeRow) * bp.mode[m].merge.size());
-  }
+  const bool staged[2] = {true, true};  // the mask is chosen at run time
+  const HeapPlace hp = place_lists(bp, npages, staged);
+  size_t bytes = 0;
+  if (write_image(h, l, hp, L.sh, bp, pages, npages, bytes, err) != FE_OK) return fail(FE_ECAPACITY, err);
+  // One copy: the fixed regions and the used part of the heap.
+  hipError_t e = hipMemcpyAsync(p->dev, h, bytes, hipMemcpyHostToDevice, st);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
   e = hipEventRecord(p->staged, st);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
@@ -553,7 +622,7 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
     p->graph_nc = graph_nc;
     L.graph_tile = graph_tile;
   }
-  record_lists(L, bp, nc);
+  record_lists(L, bp, hp, nc);
   return FE_OK;
 }
 
