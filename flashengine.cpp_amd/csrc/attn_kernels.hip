@@ -19,6 +19,9 @@
 //    accumulation (chunked prefill, DFlash blocks, verify rows).
 //  * attn_merge_kernel: combines split-KV partials by their log-sum-exp, one
 //    wavefront per (query row, head) with a batch of splits in flight.
+// and stage_copy_kernel, which moves a prepared plan's metadata from pinned
+// host memory into its device arena on the caller's stream.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -822,6 +825,24 @@ static hipError_t decode_launch_waves(const AttnArgs& a, int waves, int ncb, int
 hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int causal, int grid, hipStream_t st) {
   return bf16 ? decode_launch_waves<true>(a, waves, ncb, causal, grid, st)
               : decode_launch_waves<false>(a, waves, ncb, causal, grid, st);
+}
+
+// Plan staging: copies a prepared metadata image from pinned host memory
+// (read through its device mapping) into the plan's device arena, as a
+// kernel on the caller's stream.  A copy-engine transfer there costs about
+// 20 us a step: the copy engine waits for the compute queue's previous
+// kernels and the next kernel waits for the copy engine.  16 bytes per lane.
+__global__ __launch_bounds__(256) void stage_copy_kernel(u32x4* dst, const u32x4* src, int n16) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n16; i += gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_stage_copy(void* dst, const void* src, size_t bytes, hipStream_t st) {
+  if (bytes % 16 != 0 || bytes / 16 > (size_t)INT32_MAX) return hipErrorInvalidValue;
+  const int n16 = (int)(bytes / 16);
+  const int grid = std::max(1, std::min(256, (n16 + 255) / 256));
+  hipLaunchKernelGGL(stage_copy_kernel, dim3(grid), dim3(256), 0, st, static_cast<u32x4*>(dst),
+                     static_cast<const u32x4*>(src), n16);
+  return hipGetLastError();
 }
 
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st) {

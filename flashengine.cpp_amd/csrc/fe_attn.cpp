@@ -27,6 +27,7 @@ hipError_t launch_decode(const AttnArgs& a, bool bf16, int waves, int ncb, int c
 int decode_wg_waves(int hkv);
 hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st);
+hipError_t launch_stage_copy(void* dst, const void* src, size_t bytes, hipStream_t st);
 hipError_t launch_rope(void* q, void* k, const int64_t* pos, const float* cache, int rows, int hq, int hkv, int dim,
                        bool bf16, int max_pos, hipStream_t st);
 hipError_t launch_store(const void* k, const void* v, void* kc, void* vc, const int64_t* slots, int rows, int width,
@@ -495,6 +496,7 @@ struct fe_attn_plan {
   Launch run;                  // arena pointers, shape and launch sizes
   uint8_t* dev = nullptr;      // metadata arena
   uint8_t* host = nullptr;     // pinned mirror
+  uint8_t* host_dev = nullptr; // its address in the device's view
   uint16_t* part_o = nullptr;  // 16-bit partial rows
   float* part_lse = nullptr;
   hipEvent_t staged = nullptr;
@@ -535,9 +537,14 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch, int m
     return fail(code, msg);
   };
   if (hipMalloc(&p->dev, total) != hipSuccess) return cleanup(FE_ENOMEM, "hipMalloc(plan metadata) failed");
-  if (hipHostMalloc(&p->host, total, hipHostMallocDefault) != hipSuccess)
+  // Coherent and mapped: the staging kernel reads the mirror over the bus,
+  // and no device cache may keep a previous prepare's image.
+  if (hipHostMalloc(&p->host, total, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipHostMalloc(plan staging) failed");
   std::memset(p->host, 0, total);
+  if (hipHostGetDevicePointer(reinterpret_cast<void**>(&p->host_dev), p->host, 0) != hipSuccess ||
+      p->host_dev == nullptr)
+    return cleanup(FE_EDEVICE, "hipHostGetDevicePointer(plan staging) failed");
   if (hipMalloc(&p->part_o, (size_t)sh.partial_cap * hq * kHeadDim * sizeof(uint16_t)) != hipSuccess)
     return cleanup(FE_ENOMEM, "hipMalloc(split-KV partials) failed");
   if (hipMalloc(&p->part_lse, (size_t)sh.partial_cap * hq * sizeof(float)) != hipSuccess)
@@ -610,9 +617,10 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   const HeapPlace hp = place_lists(bp, npages, staged);
   size_t bytes = 0;
   if (write_image(h, l, hp, L.sh, bp, pages, npages, bytes, err) != FE_OK) return fail(FE_ECAPACITY, err);
-  // One copy: the fixed regions and the used part of the heap.
-  hipError_t e = hipMemcpyAsync(p->dev, h, bytes, hipMemcpyHostToDevice, st);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(plan metadata)");
+  // One transfer of the fixed regions and the used part of the heap, by a
+  // kernel on `st` that reads the mirror (no copy-engine handoff).
+  hipError_t e = launch_stage_copy(p->dev, p->host_dev, bytes, st);
+  if (e != hipSuccess) return hip_fail(e, "plan staging kernel launch");
   e = hipEventRecord(p->staged, st);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
   p->staged_pending = true;

@@ -67,9 +67,9 @@ int fe_attn_plan_destroy(fe_attn_plan* plan);
  * Validates the host CSR metadata (batch <= max_batch, kv[batch] <=
  * max_batch*max_pages, qlen <= len <= (max_pages-1)*page, page ids in
  * [0, blocks], last in [1, page]), builds the decode / tile / merge work
- * lists and copies them to the plan's device buffers on `stream` (one
- * host-to-device copy from the plan's pinned staging memory; the call
- * waits for the previous prepare's copy before reusing it).
+ * lists and copies them to the plan's device buffers on `stream` (one small
+ * kernel on `stream` reads the plan's pinned staging memory; the call waits
+ * for the previous prepare's transfer before reusing that memory).
  * `graph` != 0 pins the launch grids to the plan capacity so that a graph
  * captured once replays correctly after later prepares.  `stream` must be
  * on the device that was current when the plan was created (FE_EDEVICE
