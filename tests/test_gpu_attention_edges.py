@@ -267,6 +267,37 @@ def test_graph_captured_on_blocks(dev):
     plan.close()
 
 
+def test_back_to_back_prepares_without_host_sync(dev):
+    """One plan prepared for two different batches in turn, each prepare
+    followed by its attention call, 12 times with no host synchronisation:
+    a prepare rewrites the plan's pinned staging image only after the
+    previous prepare's staging kernel has read it, so every call sees its
+    own metadata.  Each call writes its own output buffer; all match the
+    oracle afterwards."""
+    hq, hkv, blocks = 32, 8, 1200
+    a = W.make_batch(hq, hkv, starts=[3000, 17, 900, 2500], qlens=[1, 1, 5, 1], seed=61, pool=blocks)
+    b = W.make_batch(hq, hkv, starts=[64, 4000, 1200], qlens=[40, 1, 16], seed=62, pool=blocks)
+    # one K/V pool serves both batches: their pages come from the same pool of `blocks`
+    q, kc, vc = W.make_tensors(a, seed=61)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    qb = torch.randn(b.rows, hq, 128, generator=torch.Generator().manual_seed(62)).to(torch.bfloat16)
+    qbd = qb.to(dev)
+    plan = feattn.Plan(hq, hkv, 128, 16, 4, 300, True, blocks)
+    outs = []
+    for i in range(12):
+        bb, qq = (a, qd) if i % 2 == 0 else (b, qbd)
+        plan.prepare(bb.qo, bb.kv, bb.pages, bb.last, bb.batch, bb.rows)
+        out = torch.empty_like(qq)
+        lse = torch.empty(bb.rows, hq, device=dev)
+        plan.run(qq, kd, vd, out, causal=True, lse=lse)
+        outs.append((bb, out, lse))
+    torch.cuda.synchronize()
+    plan.close()
+    want = {id(a): A.run(a, q, kc, vc, True), id(b): A.run(b, qb, kc, vc, True)}
+    for bb, out, lse in outs:
+        check(out.cpu(), lse.cpu(), *want[id(bb)])
+
+
 def test_misaligned_tensors_are_refused(dev):
     """q, the K/V caches and out move in 16-byte pieces: a view starting 8
     bytes into its storage is refused before any launch, and the aligned
