@@ -810,8 +810,8 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch, int max
   return FE_OK;
 }
 
-int fe_attn_assign_shares(const int32_t* costs, int n, int slots, int32_t* order_out, int32_t* off_out,
-                          int* n_shares_out) {
+int fe_attn_assign_shares(const int32_t* costs, int n, int slots, int fast, int32_t* order_out,
+                          int32_t* off_out, int* n_shares_out) {
   if (n < 0 || slots < 1 || slots >= (1 << 20)) return fail(FE_EINVAL, "assign_shares: n >= 0 and 1 <= slots < 2^20");
   if (n > 0 && (costs == nullptr || order_out == nullptr)) return fail(FE_EINVAL, "assign_shares: null pointer");
   if (off_out == nullptr || n_shares_out == nullptr) return fail(FE_EINVAL, "assign_shares: null pointer");
@@ -824,7 +824,7 @@ int fe_attn_assign_shares(const int32_t* costs, int n, int slots, int32_t* order
   }
   if (total >= (int64_t(1) << 43)) return fail(FE_EINVAL, "assign_shares: total cost must stay below 2^43");
   std::vector<int32_t> off;
-  assign_shares(items, slots, off);
+  assign_shares(items, slots, off, fast < 0 ? (1 << 30) : fast);
   for (int i = 0; i < n; ++i) order_out[i] = items[i].seq;
   for (size_t k = 0; k < off.size(); ++k) off_out[k] = off[k];
   *n_shares_out = (int)off.size() - 1;

@@ -37,7 +37,7 @@ std::vector<int64_t> cut_uniform(int64_t stream, int64_t quota) {
 // processing time rule -- in decreasing cost order, each item goes to the
 // least-loaded share -- and regroups them share by share (longest first
 // inside a share).  off receives the CSR offsets of the shares in use.
-void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off) {
+void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off, int fast) {
   // Stable sort by decreasing cost: a counting sort over the (small,
   // non-negative) costs, else the comparison sort.
   int32_t cmin = 0, cmax = 0;
@@ -60,13 +60,18 @@ void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>
   std::vector<int> share(items.size());
   // Binary min-heap of (load << 20 | share) keys: the root is the least-loaded
   // share, the lowest index among equals.  Each item raises the root's load
-  // and sifts it down (one pass instead of a pop and a push).
+  // and sifts it down (one pass instead of a pop and a push).  Shares below
+  // `fast` count their load at kFastShareWeight / kSlowShareWeight (2/3): they
+  // end up with 3/2 of the others' work.
   constexpr int kShareBits = 20;  // shares (tile workgroups) < 2^20; loads < 2^43
+  const bool weighted = fast < n;
   std::vector<uint64_t> heap(n);
   for (int k = 0; k < n; ++k) heap[k] = (uint64_t)k;  // ascending: already a heap
   for (size_t i = 0; i < items.size(); ++i) {
-    share[i] = (int)(heap[0] & ((uint64_t(1) << kShareBits) - 1));
-    const uint64_t key = heap[0] + ((uint64_t)items[i].cost << kShareBits);
+    const int k = (int)(heap[0] & ((uint64_t(1) << kShareBits) - 1));
+    share[i] = k;
+    const uint64_t w = !weighted ? 1 : (k < fast ? kFastShareWeight : kSlowShareWeight);
+    const uint64_t key = heap[0] + (((uint64_t)items[i].cost * w) << kShareBits);
     size_t h = 0;
     for (;;) {
       size_t c = 2 * h + 1;
@@ -445,7 +450,14 @@ static int build_plan_impl(const PlanShape& sh, const int32_t* qo, const int32_t
       }
       want = std::max(1, want / 2);
     }
-    assign_shares(ml.tile, sh.tile_slots, ml.tile_off);
+    // Two tile workgroups share each CU; the first of the pair to be
+    // dispatched (workgroup b < num_cus) wins the SIMDs' issue arbitration
+    // and, at equal work, finished the 8192-token prefill in 184 us against
+    // 230 us for the second.  The first ones therefore get more of the work:
+    // 3/2 of the second's measured fastest (0.261 against 0.267 ms for equal
+    // shares; 4/3 gained 1 %, 2/1 lost), since the second speeds up once its
+    // partner has finished.
+    assign_shares(ml.tile, sh.tile_slots, ml.tile_off, sh.num_cus);
     // When the longest-first list had to split chunks anyway, an equal cut
     // of the tile stream balances the workgroups to within a tile, usually
     // with fewer pieces; it replaces the list if it needs no more partial rows.

@@ -48,8 +48,13 @@ struct BuiltPlan {
 // Longest-processing-time assignment of items (by `cost`, >= 0) to at most
 // `slots` (< 2^20) shares: items in decreasing cost order (ties keep their
 // order) each go to the least-loaded share, the lowest index among equals;
-// `items` is regrouped share by share and `off` gets the CSR offsets.
-void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off);
+// `items` is regrouped share by share and `off` gets the CSR offsets.  When
+// `fast` is below the number of shares in use, shares [0, fast) are taken to
+// work kSlowShareWeight / kFastShareWeight times as fast as the rest: their
+// loads are counted at that ratio, so they receive that much more work.
+constexpr uint64_t kFastShareWeight = 2;
+constexpr uint64_t kSlowShareWeight = 3;
+void assign_shares(std::vector<WorkItem>& items, int slots, std::vector<int32_t>& off, int fast = 1 << 30);
 
 // Returns 0 (FE_OK) or a negative FE_E* code with `err` set.
 int validate_shape(const PlanShape& sh, std::string& err);

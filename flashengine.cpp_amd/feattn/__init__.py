@@ -93,7 +93,7 @@ def lib() -> ctypes.CDLL:
     L.fe_attn_plan_prepare.argtypes = [_vp, _i32p, _i32p, _i32p, _i32p, _int, _int, _int, _vp]
     L.fe_attn_run.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
     L.fe_attn_run_noalloc.argtypes = [_vp] * 5 + [_int] + [_i32p] * 4 + [_int] * 8 + [_vp]
-    L.fe_attn_assign_shares.argtypes = [_i32p, _int, _int, _i32p, _i32p, ctypes.POINTER(_int)]
+    L.fe_attn_assign_shares.argtypes = [_i32p, _int, _int, _int, _i32p, _i32p, ctypes.POINTER(_int)]
     L.fe_rope.argtypes = [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _int]
     L.fe_store.argtypes = [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp, _int]
     L.fe_rope_append.argtypes = [_vp] * 8 + [_int] * 7 + [_vp]
@@ -236,14 +236,15 @@ def describe(hq, hkv, dim, page, max_batch, max_pages, blocks, qo, kv, pages, la
     return tuple(out)
 
 
-def assign_shares(costs: Sequence[int], slots: int):
+def assign_shares(costs: Sequence[int], slots: int, fast: int = -1):
     """Host-only planner share assignment: (order, off) -- the input index of
-    each item share by share, and the CSR offsets of the shares."""
+    each item share by share, and the CSR offsets of the shares.  Shares
+    below `fast` (when it is >= 0) take 3/2 of the others' work."""
     n = len(costs)
     order = (ctypes.c_int32 * max(1, n))()
     off = (ctypes.c_int32 * (min(slots, n) + 2))()
     ns = _int()
-    _check(lib().fe_attn_assign_shares(_i32(costs), n, slots, order, off, ctypes.byref(ns)))
+    _check(lib().fe_attn_assign_shares(_i32(costs), n, slots, fast, order, off, ctypes.byref(ns)))
     return list(order[:n]), list(off[:ns.value + 1])
 
 

@@ -178,11 +178,16 @@ int fe_attn_plan_dump(int hq, int hkv, int dim, int page, int max_batch,
  * (one share per tile workgroup), on caller-chosen costs, for tests.  Longest
  * processing time: items in decreasing cost order (equal costs keep their
  * input order) each go to the least-loaded share, the lowest index among
- * equals.  costs[n] >= 0, total below 2^43, 1 <= slots < 2^20.  Writes
- * order_out[n] (input index of each item, share by share) and
- * off_out[0..*n_shares_out] (CSR offsets of the max(1, min(slots, n))
- * shares; off_out must hold min(slots, n) + 2 entries). */
-int fe_attn_assign_shares(const int32_t* costs, int n, int slots,
+ * equals.  When 0 <= fast < the number of shares in use, the loads of shares
+ * [0, fast) count at 2/3 (they stand for the first-dispatched workgroup of
+ * each CU's pair, which runs faster), so they receive 3/2 of the work;
+ * fe_attn_plan_prepare passes the device's CU count.  fast < 0 (or >= the
+ * shares in use) weighs all shares alike.  costs[n] >= 0, total below 2^43,
+ * 1 <= slots < 2^20.  Writes order_out[n] (input index of each item, share by
+ * share) and off_out[0..*n_shares_out] (CSR offsets of the
+ * max(1, min(slots, n)) shares; off_out must hold min(slots, n) + 2
+ * entries). */
+int fe_attn_assign_shares(const int32_t* costs, int n, int slots, int fast,
                           int32_t* order_out, int32_t* off_out,
                           int* n_shares_out);
 

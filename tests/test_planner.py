@@ -180,16 +180,20 @@ def test_empty_batch_and_zero_row_sequence():
     assert all(it[1] == 1 for it in items)
 
 
-def lpt_reference(costs, slots):
+def lpt_reference(costs, slots, fast=-1):
     """Longest processing time, stated directly: items in decreasing cost
     order (ties in input order), each to the least-loaded share (lowest index
-    among equals); then grouped share by share in that order."""
+    among equals); then grouped share by share in that order.  With
+    0 <= fast < shares, a share below `fast` is loaded as if it worked 3/2 as
+    fast: its load is compared at 2/3 (as 2 * load against 3 * load)."""
     n = len(costs)
     m = max(1, min(slots, n))
+    weighted = 0 <= fast < m
+    weight = [(2 if s < fast else 3) if weighted else 1 for s in range(m)]
     order = sorted(range(n), key=lambda i: -costs[i])  # sorted() is stable
     loads, share = [0] * m, {}
     for i in order:
-        k = min(range(m), key=lambda s: (loads[s], s))
+        k = min(range(m), key=lambda s: (loads[s] * weight[s], s))
         share[i] = k
         loads[k] += costs[i]
     grouped = [i for k in range(m) for i in order if share[i] == k]
@@ -230,6 +234,34 @@ def test_share_assignment_matches_lpt_rule(case):
         assert c == sorted(c, reverse=True)
     if costs and case != "over_65536":
         assert max(loads) <= sum(costs) / min(slots, len(costs)) + max(costs)  # the LPT bound
+
+
+@pytest.mark.parametrize("fast", [0, 1, 256, 511, 512, 4000])
+def test_weighted_share_assignment(fast):
+    """Shares below `fast` (the first-dispatched workgroup of each CU's pair)
+    take 3/2 of the work of the others; `fast` outside [0, shares) weighs all
+    shares alike."""
+    rng = np.random.default_rng(5)
+    slots = 512
+    costs = rng.integers(1, 60, size=6000).tolist()
+    order, off = feattn.assign_shares(costs, slots, fast)
+    want_order, want_off, loads = lpt_reference(costs, slots, fast)
+    assert order == want_order and off == want_off
+    if fast >= slots:
+        assert (order, off) == feattn.assign_shares(costs, slots)
+    elif 0 < fast:
+        # weighted loads level out to within one item: 2 * fast load ~ 3 * slow load
+        quick = [2 * x for x in loads[:fast]]
+        slow = [3 * x for x in loads[fast:]]
+        spread = max(quick + slow) - min(quick + slow)
+        assert spread <= 3 * max(costs)
+        ratio = (sum(loads[:fast]) / fast) / (sum(loads[fast:]) / (slots - fast))
+        assert abs(ratio - 1.5) < 0.05
+    # a different assignment from the unweighted rule whenever the weights differ
+    if 0 < fast < slots:
+        assert (order, off) != feattn.assign_shares(costs, slots)
+    elif fast == 0:  # every share weighted alike
+        assert (order, off) == feattn.assign_shares(costs, slots)
 
 
 def test_share_assignment_rejects_bad_input():
