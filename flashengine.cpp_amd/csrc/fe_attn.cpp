@@ -581,6 +581,15 @@ int fe_attn_plan_prepare(fe_attn_plan* p, const int32_t* qo, const int32_t* kv, 
   std::string err;
   int rc = check_stream_device(static_cast<hipStream_t>(stream), p->device);
   if (rc != FE_OK) return rc;
+  // A captured prepare would leave its staging kernel in the graph, reading
+  // whatever the pinned image holds at each replay, and the wait on the
+  // previous transfer would name an event recorded inside the capture.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const hipError_t ce = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
+  if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(FE_EINVAL, "prepare_plan: the stream is capturing a graph; prepare outside the capture and "
+                           "capture only the attention calls");
   rc = build_plan(L.sh, qo, kv, pages, last, batch, rows, bp, err);
   if (rc != FE_OK) return fail(rc, err);
   int nc = bp.decode_nc;

@@ -63,7 +63,8 @@ int fe_attn_plan_create(int hq, int hkv, int dim, int page, int max_batch,
 int fe_attn_plan_destroy(fe_attn_plan* plan);
 
 /* Replaces fe::cuda::prepare_plan (native_cuda.hpp:9,
- * flashinfer_attention.cu:29-34, portable_gpu_ops.cpp:27-38).
+ * flashinfer_attention.cu:29-34, portable_gpu_ops.cpp:27-38).  On a stream
+ * that is capturing a graph it returns FE_EINVAL and enqueues nothing.
  * Validates the host CSR metadata (batch <= max_batch, kv[batch] <=
  * max_batch*max_pages, qlen <= len <= (max_pages-1)*page, page ids in
  * [0, blocks], last in [1, page]), builds the decode / tile / merge work

@@ -298,6 +298,30 @@ def test_back_to_back_prepares_without_host_sync(dev):
         check(out.cpu(), lse.cpu(), *want[id(bb)])
 
 
+def test_prepare_refuses_a_capturing_stream(dev):
+    """prepare_plan on a capturing stream returns FE_EINVAL before enqueuing
+    anything; the capture ends with an empty graph, and the plan still holds
+    the metadata of its previous prepare."""
+    a = W.make_batch(32, 8, starts=[100, 40], qlens=[1, 3], seed=71)
+    b = W.make_batch(32, 8, starts=[900, 5], qlens=[2, 1], seed=72)
+    q, kc, vc = W.make_tensors(a, seed=71)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    plan = feattn.Plan(32, 8, 128, 16, 2, max(a.max_pages(), b.max_pages()), True, a.blocks)
+    plan.prepare(a.qo, a.kv, a.pages, a.last, a.batch, a.rows)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="thread_local"):
+        with pytest.raises(RuntimeError, match="capturing"):
+            plan.prepare(b.qo, b.kv, b.pages, b.last, b.batch, b.rows)
+    torch.cuda.synchronize()
+    out = torch.zeros_like(qd)
+    lse = torch.empty(a.rows, 32, device=dev)
+    plan.run(qd, kd, vd, out, causal=True, lse=lse)
+    torch.cuda.synchronize()
+    plan.close()
+    check(out.cpu(), lse.cpu(), *A.run(a, q, kc, vc, True))
+
+
 def test_misaligned_tensors_are_refused(dev):
     """q, the K/V caches and out move in 16-byte pieces: a view starting 8
     bytes into its storage is refused before any launch, and the aligned
