@@ -220,7 +220,7 @@ def test_rope_append_full_prefill_step(dev, bf16):
     args = lambda *t: [x.to(dev) for x in t]
     qd, kd, vd, kcd, vcd, posd, slotsd, tabd = args(q, k, v, kc, vc, pos, slots, table)
     feattn.rope_append(qd, kd, vd, kcd, vcd, posd, slotsd, tabd, b.rows, 32, 8, 128, bf16, 4096, b.cache_slots)
-    q2, k2, kc2, vc2 = qd.new_tensor(q), kd.new_tensor(k), kcd.new_tensor(kc), vcd.new_tensor(vc)
+    q2, k2, kc2, vc2 = args(q, k, kc, vc)  # fresh device copies of the unrotated inputs
     feattn.rope(q2, k2, posd, tabd, b.rows, 32, 8, 128, bf16, 4096)
     feattn.store(k2, vd, kc2, vc2, slotsd, b.rows, 8 * 128, bf16, b.cache_slots)
     torch.cuda.synchronize()
