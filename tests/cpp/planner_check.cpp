@@ -3,8 +3,11 @@
 // several head layouts and page sizes) must plan into work lists whose every
 // index stays inside the lists, the sequences and the partial workspace, and
 // whose pieces cover each (query rows, kv head) token range exactly once;
-// corrupted metadata must be refused with an error code.  Built and run by
-// tests/test_planner_sanitized.py (g++ with -fsanitize=address,undefined).
+// corrupted metadata must be refused with an error code.  A second pass runs
+// serving steps through the host driver (the FIFO page allocator and the
+// per-step metadata builder, graph padding included) into the planner.
+// Built and run by tests/test_planner_sanitized.py (g++ with
+// -fsanitize=address,undefined).
 #include <stdint.h>
 #include <stdio.h>
 
@@ -14,7 +17,17 @@
 #include <vector>
 
 #include "fe_attn.h"
+#include "fe_driver.h"
 #include "planner.hpp"
+
+namespace feattn {
+// The library's error reporter lives with the HIP entry points; the host
+// code under test only needs its contract (returns `code`).
+int report_error(int code, const std::string& msg) {
+  (void)msg;
+  return code;
+}
+}  // namespace feattn
 
 using namespace feattn;
 
@@ -214,6 +227,103 @@ bool check_refused(const Batch& good, std::mt19937& rng) {
   return true;
 }
 
+// Serving steps: sequences arrive (a prefill chunk), decode a token per step
+// or take another chunk, and finish; every step's metadata comes from the
+// page allocator and fe_prepare_metadata (padded to a graph bucket at times)
+// and must plan cleanly.
+bool serve(std::mt19937& rng, int steps, int& planned) {
+  const int page = 16, pool = 3000;
+  fe_blocks* blocks = nullptr;
+  CHECK(fe_blocks_create(pool, page, &blocks) == FE_OK, "allocator");
+  struct Seq {
+    int64_t id, len;
+  };
+  std::vector<Seq> live;
+  int64_t next_id = 0;
+  for (int step = 0; step < steps; ++step) {
+    // arrivals and departures
+    if (live.size() < 40 && rng() % 2 == 0) live.push_back(Seq{next_id++, 0});
+    if (!live.empty() && rng() % 5 == 0) {
+      const size_t k = rng() % live.size();
+      CHECK(fe_blocks_release(blocks, live[k].id) == FE_OK, "release");
+      live.erase(live.begin() + (long)k);
+    }
+    std::vector<int64_t> start;
+    std::vector<int32_t> rows, table_off(1, 0), tables;
+    std::vector<size_t> in_step;
+    for (size_t k = 0; k < live.size(); ++k) {
+      const int r = live[k].len == 0 || rng() % 6 == 0 ? 1 + (int)(rng() % 700) : 1;
+      int ok = 0;
+      CHECK(fe_blocks_ensure(blocks, live[k].id, live[k].len + r, &ok) == FE_OK, "ensure");
+      if (!ok) continue;  // the pool is full: the sequence waits
+      int n = 0;
+      CHECK(fe_blocks_table(blocks, live[k].id, nullptr, 0, &n) == FE_OK, "table size");
+      const size_t at = tables.size();
+      tables.resize(at + (size_t)n);
+      int n2 = 0;
+      CHECK(fe_blocks_table(blocks, live[k].id, tables.data() + at, n, &n2) == FE_OK && n2 == n, "table");
+      start.push_back(live[k].len);
+      rows.push_back(r);
+      table_off.push_back((int32_t)tables.size());
+      in_step.push_back(k);
+    }
+    int64_t held = 0;
+    for (const Seq& q : live) {
+      int n = 0;
+      fe_blocks_table(blocks, q.id, nullptr, 0, &n);
+      held += n;
+    }
+    CHECK(held == fe_blocks_used(blocks), "allocator: %lld pages in tables, %lld used", (long long)held,
+          (long long)fe_blocks_used(blocks));
+    const int n_seqs = (int)start.size();
+    const int count = n_seqs + (rng() % 3 == 0 ? (int)(rng() % 4) : 0);  // graph padding entries
+    if (count == 0) continue;
+    int n_rows = 0, n_pages = 0;
+    CHECK(fe_prepare_metadata(n_seqs, start.data(), rows.data(), table_off.data(), tables.data(), count, 1, page,
+                              1 << 20, pool, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr, &n_rows,
+                              &n_pages) == FE_OK,
+          "metadata size");
+    Batch b;
+    std::vector<int64_t> pos((size_t)n_rows), slots((size_t)n_rows);
+    b.qo.resize((size_t)count + 1);
+    b.kv.resize((size_t)count + 1);
+    b.pages.resize((size_t)n_pages);
+    b.last.resize((size_t)count);
+    CHECK(fe_prepare_metadata(n_seqs, start.data(), rows.data(), table_off.data(), tables.data(), count, 1, page,
+                              1 << 20, pool, pos.data(), slots.data(), n_rows, b.qo.data(), b.kv.data(), b.pages.data(),
+                              n_pages, b.last.data(), nullptr, nullptr) == FE_OK,
+          "metadata");
+    // each written slot lies in a page of its own sequence's table
+    for (int i = 0; i < n_seqs; ++i)
+      for (int j = 0; j < rows[i]; ++j) {
+        const int64_t r = b.qo[i] + j;
+        CHECK(pos[r] == start[i] + j, "position of row %lld", (long long)r);
+        CHECK(slots[r] == (int64_t)tables[table_off[i] + pos[r] / page] * page + pos[r] % page, "slot of row %lld",
+              (long long)r);
+      }
+    b.hq = 32;
+    b.hkv = 8;
+    b.page = page;
+    b.blocks = pool;  // the padding entries' dummy page
+    b.max_batch = count;
+    int maxp = 1;
+    for (int i = 0; i < count; ++i) maxp = std::max(maxp, b.kv[i + 1] - b.kv[i]);
+    b.max_pages = maxp + 1;
+    b.rows = n_rows;
+    const PlanShape sh = shape_of(b);
+    BuiltPlan bp;
+    std::string err;
+    const int rc = build_plan(sh, b.qo.data(), b.kv.data(), b.pages.data(), b.last.data(), count, n_rows, bp, err);
+    if (rc == FE_ECAPACITY) continue;
+    CHECK(rc == FE_OK, "step %d: metadata refused by the planner: %s", step, err.c_str());
+    if (!check_plan(b, sh, bp)) return false;
+    ++planned;
+    for (size_t i = 0; i < in_step.size(); ++i) live[in_step[i]].len += rows[i];
+  }
+  fe_blocks_destroy(blocks);
+  return true;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -240,6 +350,10 @@ int main(int argc, char** argv) {
     ++refused;
   }
   if (g_fail) return 1;
-  printf("ok: %d batches planned and checked, %d corruptions refused\n", planned, refused);
+  const int steps = argc > 2 ? atoi(argv[2]) : 300;
+  int served = 0;
+  if (!serve(rng, steps, served)) return 1;
+  printf("ok: %d batches planned and checked, %d corruptions refused, %d of %d serving steps planned\n", planned,
+         refused, served, steps);
   return 0;
 }
