@@ -373,6 +373,49 @@ def test_null_lse_gives_the_same_output(dev, causal):
     check(no_lse.cpu(), lse.cpu(), want_out, want_lse)
 
 
+def test_pool_beyond_4_gib(dev):
+    """K/V caches of 140001 pages each (4.6 GB at hkv 8, 32 KB per page) with
+    every page of the batch past the first 4 GiB, so each K/V address and
+    store offset needs more than 32 bits: decode rows, a 16-row block and a
+    prefill chunk (both masks) against the oracle on a compact copy of the
+    pages, then the batch's new K/V rows stored at their slots and read back
+    bit-exact."""
+    hq, hkv, page, pool = 32, 8, 16, 140000
+    compact = W.make_batch(hq, hkv, starts=[3000, 700, 0, 1500], qlens=[1, 16, 300, 1], seed=81)
+    q, kc, vc = W.make_tensors(compact, seed=81)
+    base = pool - compact.blocks - 1  # compact page p is page base + p of the large pool
+    assert base * page * hkv * 128 * 2 > 1 << 32
+    big = W.build_metadata(W.Batch(hq=hq, hkv=hkv, page=page, blocks=pool, starts=list(compact.starts),
+                                   qlens=list(compact.qlens),
+                                   tables=[[base + p for p in t] for t in compact.tables]))
+    kd = torch.empty((pool + 1, page, hkv, 128), dtype=torch.bfloat16, device=dev)
+    vd = torch.empty_like(kd)
+    kd[base:base + compact.blocks + 1].copy_(kc.to(dev))
+    vd[base:base + compact.blocks + 1].copy_(vc.to(dev))
+    qd = q.to(dev)
+    plan = feattn.Plan(hq, hkv, 128, page, big.batch, big.max_pages(), True, big.blocks)
+    plan.prepare(big.qo, big.kv, big.pages, big.last, big.batch, big.rows)
+    for causal in (True, False):
+        out = torch.zeros_like(qd)
+        lse = torch.full((big.rows, hq), float("nan"), device=dev)
+        plan.run(qd, kd, vd, out, causal=causal, lse=lse)
+        torch.cuda.synchronize()
+        check(out.cpu(), lse.cpu(), *A.run(compact, q, kc, vc, causal))
+    plan.close()
+    gen = torch.Generator().manual_seed(82)
+    k_new = torch.randn(big.rows, hkv, 128, generator=gen).to(torch.bfloat16)
+    v_new = torch.randn(big.rows, hkv, 128, generator=gen).to(torch.bfloat16)
+    slots = torch.from_numpy(big.slots)
+    assert int(slots.min()) >= base * page
+    feattn.store(k_new.to(dev), v_new.to(dev), kd, vd, slots.to(dev), big.rows, hkv * 128, True, (pool + 1) * page)
+    torch.cuda.synchronize()
+    kflat, vflat = kd.view(-1, hkv, 128), vd.view(-1, hkv, 128)
+    sd = slots.to(dev)
+    assert torch.equal(kflat[sd].cpu(), k_new) and torch.equal(vflat[sd].cpu(), v_new)
+    del kd, vd, kflat, vflat
+    torch.cuda.empty_cache()
+
+
 def test_two_plans_on_two_streams(dev):
     """Two plans (a decode batch and a prefill batch, different shapes) are
     prepared and run on two streams at once, three times in a row; both
