@@ -52,6 +52,13 @@ DRIVER_SYMBOLS = (
     "fe_blocks_release",
     "fe_blocks_table",
     "fe_blocks_used",
+    "fe_blocks_create_ex",
+    "fe_blocks_forget",
+    "fe_blocks_free_pages",
+    "fe_blocks_set_prefix_hooks",
+    "fe_blocks_probe",
+    "fe_blocks_publish",
+    "fe_blocks_prefix_stats",
     "fe_prepare_metadata",
     "fe_rope_table",
 )
@@ -69,6 +76,12 @@ _LIB: Optional[ctypes.CDLL] = None
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _vp = ctypes.c_void_p
 _int = ctypes.c_int
+
+
+class PrefixStats(ctypes.Structure):
+    """fe_prefix_stats (include/fe_driver.h)."""
+    _fields_ = [(name, ctypes.c_int64) for name in (
+        "requests", "hit_requests", "cached_blocks", "new_blocks", "resident_blocks", "evictions")]
 
 
 def lib() -> ctypes.CDLL:
@@ -112,12 +125,19 @@ def lib() -> ctypes.CDLL:
     L.fe_blocks_release.argtypes = [_vp, _i64]
     L.fe_blocks_table.argtypes = [_vp, _i64, _i32p, _int, ctypes.POINTER(_int)]
     L.fe_blocks_used.argtypes = [_vp]
+    L.fe_blocks_create_ex.argtypes = [_i64, _i64, _int, ctypes.POINTER(_vp)]
+    L.fe_blocks_forget.argtypes = [_vp, _i64]
+    L.fe_blocks_free_pages.argtypes = [_vp]
+    L.fe_blocks_set_prefix_hooks.argtypes = [_vp, _vp, _vp, _vp]
+    L.fe_blocks_probe.argtypes = [_vp, _i64, _i64p, _i64, _i64p]
+    L.fe_blocks_publish.argtypes = [_vp, _i64, _i64p, _i64, _i64]
+    L.fe_blocks_prefix_stats.argtypes = [_vp, ctypes.POINTER(PrefixStats)]
     L.fe_prepare_metadata.argtypes = ([_int, _i64p, _i32p, _i32p, _i32p, _int, _int, _int, _i64, ctypes.c_int32,
                                        _i64p, _i64p, _int, _i32p, _i32p, _i32p, _int, _i32p,
                                        ctypes.POINTER(_int), ctypes.POINTER(_int)])
     L.fe_rope_table.argtypes = [_vp, _int, _int, ctypes.c_double, _vp]
     for name in DRIVER_SYMBOLS:
-        getattr(L, name).restype = _i64 if name == "fe_blocks_used" else _int
+        getattr(L, name).restype = _i64 if name in ("fe_blocks_used", "fe_blocks_free_pages") else _int
     _f = ctypes.c_float
     L.fe_norm.argtypes = [_vp] * 5 + [_int, _int, _f, _int, _vp]
     L.fe_silu_mul.argtypes = [_vp, _vp, _int, _int, _int, _vp]
@@ -279,14 +299,58 @@ def graph_buckets(maximum: int):
     return list(out[:n.value])
 
 
-class Blocks:
-    """FIFO KV page allocator: the page-table side of fe::BlockManager
-    (src/scheduler.cpp:5,31-35), sequences keyed by an integer id."""
+_READY_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int64,
+                             ctypes.c_int32)
+_EVICT_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int64,
+                             ctypes.c_int32)
 
-    def __init__(self, total: int, block_size: int):
+
+def _tokens(tokens):
+    arr = (ctypes.c_int64 * max(1, len(tokens)))(*[int(t) for t in tokens])
+    return arr, len(tokens)
+
+
+class Blocks:
+    """FIFO KV page allocator with its prefix cache: fe::BlockManager
+    (src/scheduler.cpp:5-36), sequences keyed by an integer id.  `ready(key,
+    page)` / `evict(key, page)` (key a tuple of token ids) stand for the
+    reference's prefix_page_ready / on_evict_page hooks."""
+
+    def __init__(self, total: int, block_size: int, caching: bool = False):
         handle = _vp()
-        _check(lib().fe_blocks_create(total, block_size, ctypes.byref(handle)))
+        _check(lib().fe_blocks_create_ex(total, block_size, int(bool(caching)), ctypes.byref(handle)))
         self._h = handle
+        self._hooks = None
+
+    def set_hooks(self, ready=None, evict=None) -> None:
+        r = _READY_FN(lambda _u, key, n, page: int(bool(ready(tuple(key[:n]), page)))) if ready else None
+        e = _EVICT_FN(lambda _u, key, n, page: evict(tuple(key[:n]), page)) if evict else None
+        _check(lib().fe_blocks_set_prefix_hooks(self._h, ctypes.cast(r, _vp) if r else None,
+                                                ctypes.cast(e, _vp) if e else None, None))
+        self._hooks = (r, e)  # the library holds raw pointers to these
+
+    def probe(self, seq: int, tokens) -> int:
+        arr, n = _tokens(tokens)
+        cached = ctypes.c_int64()
+        _check(lib().fe_blocks_probe(self._h, seq, arr, n, ctypes.byref(cached)))
+        return cached.value
+
+    def publish(self, seq: int, tokens, computed: int) -> None:
+        arr, n = _tokens(tokens)
+        _check(lib().fe_blocks_publish(self._h, seq, arr, n, computed))
+
+    def forget(self, seq: int) -> None:
+        _check(lib().fe_blocks_forget(self._h, seq))
+
+    def free_pages(self) -> int:
+        return lib().fe_blocks_free_pages(self._h)
+
+    def stats(self) -> dict:
+        st = PrefixStats()
+        _check(lib().fe_blocks_prefix_stats(self._h, ctypes.byref(st)))
+        return {"prefix_requests": st.requests, "prefix_hit_requests": st.hit_requests,
+                "prefix_cached_blocks": st.cached_blocks, "prefix_new_blocks": st.new_blocks,
+                "prefix_resident_blocks": st.resident_blocks, "prefix_evictions": st.evictions}
 
     def ensure(self, seq: int, target_tokens: int) -> bool:
         ok = _int()

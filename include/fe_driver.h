@@ -4,9 +4,9 @@
  *
  *   fe_graph_buckets     batch sizes that get a captured HIP graph
  *                        (reference src/common.cpp:45-51)
- *   fe_blocks_*          FIFO KV page allocator, per sequence page tables
- *                        (reference src/scheduler.cpp:5,31-35, BlockManager
- *                        without the prefix cache)
+ *   fe_blocks_*          FIFO KV page allocator, per sequence page tables,
+ *                        and its prefix cache of shared read-only pages
+ *                        (reference src/scheduler.cpp:5-36, BlockManager)
  *   fe_prepare_metadata  per-step positions / slots and the CSR metadata that
  *                        fe_attn_plan_prepare consumes, graph padding included
  *                        (reference src/cuda_model.cpp:131-142)
@@ -33,26 +33,87 @@ extern "C" {
 int fe_graph_buckets(int64_t maximum, int64_t* out, int cap, int* n_out);
 
 /* KV page allocator, the page-table side of fe::BlockManager (reference
- * src/scheduler.cpp:5 constructor, :31 ensure, :35 release; the prefix cache
- * is not part of this path).  Free pages form a FIFO queue that starts as
+ * src/scheduler.cpp:5 constructor, :31 ensure, :36 release, :6 probe, :18
+ * publish, :30 snapshot).  Free pages form a FIFO queue that starts as
  * 0, 1, ..., total-1; ensure takes pages from its front, release returns a
- * sequence's pages to its back. */
+ * sequence's pages to its back once no sequence holds them.  With the prefix
+ * cache on, a page published under the token prefix it ends stays resident
+ * after release until ensure takes it from the queue again (an eviction),
+ * and probe hands it, shared and read-only, to every later sequence whose
+ * tokens start with that prefix.  Sequences are integer ids.  Not
+ * thread-safe. */
 typedef struct fe_blocks fe_blocks;
 
-/* total in (0, INT32_MAX), block_size > 0. */
+/* total in (0, INT32_MAX), block_size > 0; no prefix cache (reference:
+ * BlockManager(total, block_size)). */
 int fe_blocks_create(int64_t total, int64_t block_size, fe_blocks** out);
+/* Same, with the prefix cache on when caching != 0 (reference:
+ * BlockManager(total, block_size, caching), src/scheduler.cpp:5). */
+int fe_blocks_create_ex(int64_t total, int64_t block_size, int caching, fe_blocks** out);
 int fe_blocks_destroy(fe_blocks* blocks);
 /* Grows sequence `seq`'s table to ceil(target_tokens / block_size) pages.
  * *ok_out = 1 on success (or nothing to do); 0, with nothing allocated, when
- * too few pages are free (reference: ensure returns false). */
+ * too few pages are free (reference: ensure returns false).  A page taken
+ * from the queue that is still resident in the prefix cache is evicted
+ * first (the evict hook is told). */
 int fe_blocks_ensure(fe_blocks* blocks, int64_t seq, int64_t target_tokens, int* ok_out);
-/* Returns all pages of `seq` to the free queue (no-op for an unknown seq). */
+/* Drops `seq`'s hold on its pages; a page no sequence holds any more goes to
+ * the back of the free queue (no-op for an unknown seq).  The sequence's
+ * probe may run again afterwards (reference: release resets cached and
+ * prefix_probed, src/scheduler.cpp:36); its request counters are kept, so a
+ * preempted request counts once in the statistics. */
 int fe_blocks_release(fe_blocks* blocks, int64_t seq);
+/* release, then forget the sequence's request counters: call it when the
+ * request finishes (the reference's Sequence object goes away). */
+int fe_blocks_forget(fe_blocks* blocks, int64_t seq);
 /* Copies up to `cap` page ids of `seq` to `out` (may be NULL) and the table
  * length to *n_out. */
 int fe_blocks_table(const fe_blocks* blocks, int64_t seq, int32_t* out, int cap, int* n_out);
-/* Pages currently allocated (reference: BlockManager::used). */
+/* Pages held by at least one sequence (reference: BlockManager::used). */
 int64_t fe_blocks_used(const fe_blocks* blocks);
+/* Pages in the free queue, resident cached pages included (reference:
+ * BlockManager::free). */
+int64_t fe_blocks_free_pages(const fe_blocks* blocks);
+
+/* Prefix-cache hooks (reference: BlockManager::prefix_page_ready and
+ * on_evict_page, bound to the model by bind_model, include/fe/model.hpp:22-26).
+ * ready(user, key, n, page) returns nonzero when the page cached under the
+ * n-token prefix `key` may be reused (probe) or published (publish); evict
+ * (user, key, n, page) is told before ensure reuses a resident page.  Either
+ * may be NULL (always ready / nothing to tell).  Hooks must not call back
+ * into the same allocator. */
+typedef int (*fe_prefix_ready_fn)(void* user, const int64_t* key, int64_t n, int32_t page);
+typedef void (*fe_prefix_evict_fn)(void* user, const int64_t* key, int64_t n, int32_t page);
+int fe_blocks_set_prefix_hooks(fe_blocks* blocks, fe_prefix_ready_fn ready, fe_prefix_evict_fn evict,
+                               void* user);
+
+/* Reference BlockManager::probe (src/scheduler.cpp:6-17): before `seq` has
+ * pages, give it the resident pages of the longest published prefix of
+ * tokens[0 .. n_tokens) that ends at least one token short of n_tokens (the
+ * last prompt token is always computed), walking block by block and stopping
+ * at the first prefix that is not resident or not ready.  *cached_out = the
+ * tokens covered (a multiple of block_size).  No-op (returning the earlier
+ * result) after a probe since the last release, and 0 with the prefix cache
+ * off.  FE_EINVAL when `seq` already holds pages. */
+int fe_blocks_probe(fe_blocks* blocks, int64_t seq, const int64_t* tokens, int64_t n_tokens, int64_t* cached_out);
+/* Reference BlockManager::publish (src/scheduler.cpp:18-29): for every full
+ * block of tokens[0 .. min(computed, n_tokens)), publish the sequence's page
+ * under the prefix it ends, unless the prefix is already resident or the
+ * ready hook says no.  FE_EINVAL (pages before it stay published) when the
+ * page is not allocated or already published under another prefix.  No-op
+ * with the prefix cache off. */
+int fe_blocks_publish(fe_blocks* blocks, int64_t seq, const int64_t* tokens, int64_t n_tokens, int64_t computed);
+
+/* Counters of BlockManager::snapshot (src/scheduler.cpp:30). */
+typedef struct fe_prefix_stats {
+  int64_t requests;        /* prefix_requests: sequences probed, once each */
+  int64_t hit_requests;    /* prefix_hit_requests: of those, with a hit */
+  int64_t cached_blocks;   /* prefix_cached_blocks: pages handed out by probe */
+  int64_t new_blocks;      /* prefix_new_blocks: pages published */
+  int64_t resident_blocks; /* prefix_resident_blocks: published, not evicted */
+  int64_t evictions;       /* prefix_evictions */
+} fe_prefix_stats;
+int fe_blocks_prefix_stats(const fe_blocks* blocks, fe_prefix_stats* out);
 
 /* Replaces CudaModel::prepare's metadata loop (reference
  * src/cuda_model.cpp:131-142).  Sequence i < n_seqs contributes rows[i]

@@ -14,14 +14,21 @@ allocator, integer-exact.
                  context outside the page table.
   graph_buckets  src/common.cpp:45-51: 1, 2, 4, 8 (<= maximum), multiples of
                  16 up to maximum, then maximum.
-  Blocks         src/scheduler.cpp:5,31,35 (BlockManager without the prefix
-                 cache): FIFO free list 0..total-1, ensure takes ceil(target /
-                 size) - held pages from the front (all or nothing), release
-                 appends a sequence's pages to the back.
+  Blocks         src/scheduler.cpp:5-36 (BlockManager): FIFO free list
+                 0..total-1, ensure takes ceil(target / size) - held pages
+                 from the front (all or nothing), evicting a resident cached
+                 page it takes; release drops a sequence's hold and appends
+                 pages no sequence holds to the back.  Prefix cache: publish
+                 maps each full block's whole token prefix to the page that
+                 ends it (a dict keyed by the prefix tuple, as the
+                 reference's map); probe walks prefixes block by block,
+                 stopping one token short of the prompt, and takes shared
+                 pages out of the free list by value.
 
-Pinned by tests/test_driver.py: graph_buckets(7) == [1, 2, 4, 7] and the
-BlockManager(2, 16) sequence of tests/host_tests.cpp:13,33, and the slot
-closed form and padding rules on hand-built cases.
+Pinned by tests/test_driver.py: graph_buckets(7) == [1, 2, 4, 7], the
+BlockManager sequences of tests/host_tests.cpp:13,33,35-46 (FIFO, prefix
+sharing, exact and stale probes, evictions and the readiness / eviction
+hooks), and the slot closed form and padding rules on hand-built cases.
 """
 
 from __future__ import annotations
@@ -40,14 +47,83 @@ def graph_buckets(maximum: int):
 
 
 class Blocks:
-    def __init__(self, total: int, size: int):
+    """src/scheduler.cpp:5-36.  Sequences are keys of `tables`; `ready(key,
+    page)` / `evict(key, page)` stand for prefix_page_ready / on_evict_page
+    (include/fe/model.hpp:24-25)."""
+
+    def __init__(self, total: int, size: int, caching: bool = False):
         if not (0 < total < 2 ** 31 - 1 and size > 0):
             raise ValueError("bad pool")
         self.size = size
+        self.caching = caching
         self.free = deque(range(total))
+        self.refs = [0] * total
         self.tables = {}
+        self.state = {}            # seq -> [cached, probed, counted, hit_counted]
+        self.cached_keys = {}      # prefix tuple -> page        (cached_)
+        self.keys = {}             # page -> prefix tuple        (keys_)
+        self.requests = self.hits = self.hit_blocks = self.new_blocks = self.evictions = 0
+        self.ready = None
+        self.evict = None
+
+    def _state(self, seq):
+        return self.state.setdefault(seq, [0, False, False, False])
+
+    def probe(self, seq, tokens) -> int:
+        # src/scheduler.cpp:6-17
+        st = self._state(seq)
+        if not self.caching or st[1]:
+            return st[0]
+        if self.tables.get(seq) or st[0]:
+            raise ValueError("prefix probe must come before allocation")
+        st[1] = True
+        if not st[2]:
+            self.requests += 1
+            st[2] = True
+        table = self.tables.setdefault(seq, [])
+        end = self.size
+        while end < len(tokens):
+            key = tuple(tokens[:end])
+            page = self.cached_keys.get(key)
+            if page is None or (self.ready is not None and not self.ready(key, page)):
+                break
+            if self.refs[page] == 0:
+                self.free.remove(page)
+            self.refs[page] += 1
+            table.append(page)
+            st[0] = end
+            self.hit_blocks += 1
+            end += self.size
+        if st[0] and not st[3]:
+            self.hits += 1
+            st[3] = True
+        return st[0]
+
+    def publish(self, seq, tokens, computed: int) -> None:
+        # src/scheduler.cpp:18-29
+        if not self.caching:
+            return
+        computed = min(computed, len(tokens))
+        table = self.tables.get(seq, [])
+        end = self.size
+        while end <= computed:
+            index = (end - 1) // self.size
+            if index >= len(table):
+                raise ValueError("publishing an unallocated KV page")
+            page, key = table[index], tuple(tokens[:end])
+            end += self.size
+            if self.ready is not None and not self.ready(key, page):
+                continue
+            if key in self.cached_keys:
+                continue
+            if page in self.keys:
+                raise ValueError("published KV pages are immutable")
+            self.cached_keys[key] = page
+            self.keys[page] = key
+            self.new_blocks += 1
 
     def ensure(self, seq, target: int) -> bool:
+        # src/scheduler.cpp:31-34
         table = self.tables.setdefault(seq, [])
         need = (target + self.size - 1) // self.size
         if need <= len(table):
@@ -55,14 +131,45 @@ class Blocks:
         if need - len(table) > len(self.free):
             return False
         while len(table) < need:
-            table.append(self.free.popleft())
+            page = self.free.popleft()
+            key = self.keys.pop(page, None)
+            if key is not None:
+                if self.evict is not None:
+                    self.evict(key, page)
+                del self.cached_keys[key]
+                self.evictions += 1
+            assert self.refs[page] == 0
+            self.refs[page] = 1
+            table.append(page)
         return True
 
     def release(self, seq) -> None:
-        self.free.extend(self.tables.pop(seq, []))
+        # src/scheduler.cpp:36
+        for page in self.tables.pop(seq, []):
+            if self.refs[page] <= 0:
+                raise ValueError("KV page released twice")
+            self.refs[page] -= 1
+            if self.refs[page] == 0:
+                self.free.append(page)
+        if seq in self.state:
+            self.state[seq][0] = 0
+            self.state[seq][1] = False
+
+    def forget(self, seq) -> None:
+        self.release(seq)
+        self.state.pop(seq, None)
 
     def used(self) -> int:
-        return sum(len(t) for t in self.tables.values())
+        return sum(1 for r in self.refs if r > 0)
+
+    def free_pages(self) -> int:
+        return len(self.free)
+
+    def stats(self) -> dict:
+        # src/scheduler.cpp:30
+        return {"prefix_requests": self.requests, "prefix_hit_requests": self.hits,
+                "prefix_cached_blocks": self.hit_blocks, "prefix_new_blocks": self.new_blocks,
+                "prefix_resident_blocks": len(self.cached_keys), "prefix_evictions": self.evictions}
 
 
 def prepare(starts, rows, tables, page: int, max_model_len: int, count=None, entry_rows: int = 0,

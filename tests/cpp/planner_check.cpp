@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <random>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "fe_attn.h"
@@ -227,54 +228,91 @@ bool check_refused(const Batch& good, std::mt19937& rng) {
   return true;
 }
 
-// Serving steps: sequences arrive (a prefill chunk), decode a token per step
-// or take another chunk, and finish; every step's metadata comes from the
-// page allocator and fe_prepare_metadata (padded to a graph bucket at times)
-// and must plan cleanly.
+// Serving steps: sequences arrive with prompts that share prefixes, take the
+// longest cached prefix from the allocator's prefix cache, prefill the rest
+// in chunks, decode a token per step, publish what they computed, are
+// preempted (their pages released and probed again) or finish; every step's
+// metadata comes from the page allocator and fe_prepare_metadata (padded to a
+// graph bucket at times) and must plan cleanly.
 bool serve(std::mt19937& rng, int steps, int& planned) {
-  const int page = 16, pool = 3000;
+  const int page = 16, pool = 1200;  // small enough for the free queue to wrap: evictions
   fe_blocks* blocks = nullptr;
-  CHECK(fe_blocks_create(pool, page, &blocks) == FE_OK, "allocator");
+  CHECK(fe_blocks_create_ex(pool, page, 1, &blocks) == FE_OK, "allocator");
   struct Seq {
     int64_t id, len;
+    std::vector<int64_t> tokens;
+    bool probed;
   };
+  std::vector<std::vector<int64_t>> stems(4);
+  for (auto& st : stems) {
+    st.resize(rng() % 700);
+    for (auto& t : st) t = (int64_t)(rng() % 4);
+  }
   std::vector<Seq> live;
-  int64_t next_id = 0;
+  int64_t next_id = 0, hits = 0;
   for (int step = 0; step < steps; ++step) {
-    // arrivals and departures
-    if (live.size() < 40 && rng() % 2 == 0) live.push_back(Seq{next_id++, 0});
+    // arrivals, departures and preemptions
+    if (live.size() < 40 && rng() % 2 == 0) {
+      Seq q{next_id++, 0, {}, false};
+      const auto& st = stems[rng() % stems.size()];
+      q.tokens.assign(st.begin(), st.begin() + (long)(rng() % (st.size() + 1)));
+      for (int t = 1 + (int)(rng() % 200); t > 0; --t) q.tokens.push_back((int64_t)(rng() % 4));
+      live.push_back(std::move(q));
+    }
     if (!live.empty() && rng() % 5 == 0) {
       const size_t k = rng() % live.size();
-      CHECK(fe_blocks_release(blocks, live[k].id) == FE_OK, "release");
+      CHECK(fe_blocks_forget(blocks, live[k].id) == FE_OK, "forget");
       live.erase(live.begin() + (long)k);
+    }
+    if (!live.empty() && rng() % 11 == 0) {
+      Seq& q = live[rng() % live.size()];
+      CHECK(fe_blocks_release(blocks, q.id) == FE_OK, "release");
+      q.len = 0;
+      q.probed = false;
     }
     std::vector<int64_t> start;
     std::vector<int32_t> rows, table_off(1, 0), tables;
     std::vector<size_t> in_step;
     for (size_t k = 0; k < live.size(); ++k) {
-      const int r = live[k].len == 0 || rng() % 6 == 0 ? 1 + (int)(rng() % 700) : 1;
+      Seq& q = live[k];
+      if (!q.probed) {
+        int64_t cached = -1;
+        CHECK(fe_blocks_probe(blocks, q.id, q.tokens.data(), (int64_t)q.tokens.size(), &cached) == FE_OK, "probe");
+        CHECK(cached % page == 0 && cached < (int64_t)q.tokens.size(), "probe covered %lld of %zu tokens",
+              (long long)cached, q.tokens.size());
+        q.len = cached;
+        q.probed = true;
+        hits += cached > 0;
+      }
+      const int64_t prompt_left = (int64_t)q.tokens.size() - q.len;
+      int r = 1;
+      if (prompt_left > 0) r = (int)std::min<int64_t>(prompt_left, 1 + (int64_t)(rng() % 700));
       int ok = 0;
-      CHECK(fe_blocks_ensure(blocks, live[k].id, live[k].len + r, &ok) == FE_OK, "ensure");
+      CHECK(fe_blocks_ensure(blocks, q.id, q.len + r, &ok) == FE_OK, "ensure");
       if (!ok) continue;  // the pool is full: the sequence waits
       int n = 0;
-      CHECK(fe_blocks_table(blocks, live[k].id, nullptr, 0, &n) == FE_OK, "table size");
+      CHECK(fe_blocks_table(blocks, q.id, nullptr, 0, &n) == FE_OK, "table size");
       const size_t at = tables.size();
       tables.resize(at + (size_t)n);
       int n2 = 0;
-      CHECK(fe_blocks_table(blocks, live[k].id, tables.data() + at, n, &n2) == FE_OK && n2 == n, "table");
-      start.push_back(live[k].len);
+      CHECK(fe_blocks_table(blocks, q.id, tables.data() + at, n, &n2) == FE_OK && n2 == n, "table");
+      start.push_back(q.len);
       rows.push_back(r);
       table_off.push_back((int32_t)tables.size());
       in_step.push_back(k);
     }
-    int64_t held = 0;
+    std::unordered_map<int32_t, int> holders;  // page -> live tables holding it
     for (const Seq& q : live) {
       int n = 0;
       fe_blocks_table(blocks, q.id, nullptr, 0, &n);
-      held += n;
+      std::vector<int32_t> t((size_t)n);
+      fe_blocks_table(blocks, q.id, t.data(), n, &n);
+      for (int32_t id : t) ++holders[id];
     }
-    CHECK(held == fe_blocks_used(blocks), "allocator: %lld pages in tables, %lld used", (long long)held,
-          (long long)fe_blocks_used(blocks));
+    CHECK((int64_t)holders.size() == fe_blocks_used(blocks) &&
+              fe_blocks_free_pages(blocks) == pool - (int64_t)holders.size(),
+          "allocator: %zu pages in tables, %lld used, %lld free", holders.size(), (long long)fe_blocks_used(blocks),
+          (long long)fe_blocks_free_pages(blocks));
     const int n_seqs = (int)start.size();
     const int count = n_seqs + (rng() % 3 == 0 ? (int)(rng() % 4) : 0);  // graph padding entries
     if (count == 0) continue;
@@ -293,13 +331,15 @@ bool serve(std::mt19937& rng, int steps, int& planned) {
                               1 << 20, pool, pos.data(), slots.data(), n_rows, b.qo.data(), b.kv.data(), b.pages.data(),
                               n_pages, b.last.data(), nullptr, nullptr) == FE_OK,
           "metadata");
-    // each written slot lies in a page of its own sequence's table
+    // each written slot lies in a page of its own sequence's table that no
+    // other sequence holds (shared prefix pages are read-only)
     for (int i = 0; i < n_seqs; ++i)
       for (int j = 0; j < rows[i]; ++j) {
         const int64_t r = b.qo[i] + j;
         CHECK(pos[r] == start[i] + j, "position of row %lld", (long long)r);
-        CHECK(slots[r] == (int64_t)tables[table_off[i] + pos[r] / page] * page + pos[r] % page, "slot of row %lld",
-              (long long)r);
+        const int32_t id = tables[table_off[i] + pos[r] / page];
+        CHECK(slots[r] == (int64_t)id * page + pos[r] % page, "slot of row %lld", (long long)r);
+        CHECK(holders[id] == 1, "row %lld writes page %d, held by %d sequences", (long long)r, id, holders[id]);
       }
     b.hq = 32;
     b.hkv = 8;
@@ -318,8 +358,19 @@ bool serve(std::mt19937& rng, int steps, int& planned) {
     CHECK(rc == FE_OK, "step %d: metadata refused by the planner: %s", step, err.c_str());
     if (!check_plan(b, sh, bp)) return false;
     ++planned;
-    for (size_t i = 0; i < in_step.size(); ++i) live[in_step[i]].len += rows[i];
+    for (size_t i = 0; i < in_step.size(); ++i) {
+      Seq& q = live[in_step[i]];
+      q.len += rows[i];
+      if (q.len > (int64_t)q.tokens.size()) q.tokens.push_back((int64_t)(rng() % 4));  // the decoded token
+      CHECK(fe_blocks_publish(blocks, q.id, q.tokens.data(), (int64_t)q.tokens.size(), q.len) == FE_OK, "publish");
+    }
   }
+  fe_prefix_stats st{};
+  CHECK(fe_blocks_prefix_stats(blocks, &st) == FE_OK && st.hit_requests > 0 && st.evictions > 0,
+        "prefix cache unexercised: %lld hits, %lld evictions", (long long)st.hit_requests, (long long)st.evictions);
+  printf("prefix cache: %lld of %lld requests hit, %lld pages reused, %lld published, %lld evicted\n",
+         (long long)st.hit_requests, (long long)st.requests, (long long)st.cached_blocks, (long long)st.new_blocks,
+         (long long)st.evictions);
   fe_blocks_destroy(blocks);
   return true;
 }

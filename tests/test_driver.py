@@ -105,6 +105,180 @@ def test_blocks_fifo_order_and_growth():
     blocks.close()
 
 
+def _blocks(impl, total, size, caching=True):
+    if impl == "native":
+        b = feattn.Blocks(total, size, caching)
+        return b, b.table
+    b = S.Blocks(total, size, caching)
+    return b, (lambda seq: b.tables.get(seq, []))
+
+
+@pytest.mark.parametrize("impl", ["native", "oracle"])
+def test_blocks_prefix_reference_assertions(impl):
+    # tests/host_tests.cpp:35-41: BlockManager(4, 16, caching)
+    cache, table = _blocks(impl, 4, 16)
+    first = same = [7] * 33
+    different = [7] * 33
+    different[1] = 9
+    assert cache.ensure(101, 33)
+    cache.publish(101, first, 32)
+    assert cache.probe(102, same) == 32
+    assert len(table(102)) == 2 and table(102)[0] == table(101)[0]
+    assert cache.ensure(102, 33)
+    assert cache.probe(103, different) == 0
+    cache.release(101)
+    assert cache.used() == 3
+    cache.release(102)
+    assert cache.used() == 0 and cache.stats()["prefix_resident_blocks"] == 2
+    cache.probe(102, same)
+    assert cache.stats()["prefix_hit_requests"] == 1       # a request counts once
+    cache.release(102)
+    assert cache.probe(104, [7] * 32) == 16 and len(table(104)) == 1   # one token left to compute
+    cache.release(104)
+    assert cache.ensure(103, 64)
+    assert cache.stats()["prefix_resident_blocks"] == 0 and cache.stats()["prefix_evictions"] == 2
+    cache.release(103)
+    assert cache.probe(105, [7] * 33) == 0 and cache.used() == 0        # evicted pages are gone
+
+
+@pytest.mark.parametrize("impl", ["native", "oracle"])
+def test_blocks_prefix_hooks_reference_assertions(impl):
+    # tests/host_tests.cpp:43-46: publication and reuse wait for the model's
+    # readiness; the model is told of evictions
+    guarded, _ = _blocks(impl, 2, 16)
+    ready, evicted = [False], []
+    if impl == "native":
+        guarded.set_hooks(ready=lambda key, page: ready[0], evict=lambda key, page: evicted.append((key, page)))
+    else:
+        guarded.ready = lambda key, page: ready[0]
+        guarded.evict = lambda key, page: evicted.append((key, page))
+    assert guarded.ensure(201, 17)
+    guarded.publish(201, [7] * 17, 16)
+    assert guarded.stats()["prefix_resident_blocks"] == 0
+    ready[0] = True
+    guarded.publish(201, [7] * 17, 16)
+    guarded.release(201)
+    ready[0] = False
+    assert guarded.probe(202, [7] * 17) == 0
+    ready[0] = True
+    assert guarded.probe(203, [7] * 17) == 16
+    guarded.release(203)
+    assert guarded.ensure(204, 32) and evicted == [(tuple([7] * 16), 0)]
+    guarded.release(204)
+
+
+def test_blocks_prefix_off_is_a_no_op():
+    # BlockManager(total, size) has caching off: probe / publish do nothing
+    blocks = feattn.Blocks(4, 16)
+    assert blocks.ensure(1, 33)
+    blocks.publish(1, [7] * 33, 32)
+    assert blocks.probe(2, [7] * 33) == 0 and blocks.table(2) == []
+    assert blocks.stats() == dict.fromkeys(S.Blocks(4, 16).stats(), 0)
+    blocks.close()
+
+
+def test_blocks_prefix_errors():
+    native, ref = feattn.Blocks(8, 4, True), S.Blocks(8, 4, True)
+    for b in (native, ref):
+        assert b.ensure(1, 8)
+    for b in (native, ref):
+        with pytest.raises((RuntimeError, ValueError), match="allocat"):
+            b.probe(1, list(range(12)))        # probe after allocation
+    for b in (native, ref):
+        with pytest.raises((RuntimeError, ValueError)):
+            b.publish(1, list(range(12)), 12)  # the third page is not allocated
+    # the pages before the failing one stay published, as in the reference
+    assert native.stats() == ref.stats() and native.stats()["prefix_new_blocks"] == 2
+    for b in (native, ref):
+        assert b.ensure(2, 8)
+    for b in (native, ref):
+        b.publish(2, list(range(100, 108)), 8)
+    for b in (native, ref):
+        with pytest.raises((RuntimeError, ValueError), match="immutable|another prefix"):
+            b.publish(2, list(range(200, 208)), 8)  # same pages, other tokens
+    assert native.stats() == ref.stats()
+    native.close()
+
+
+def _prompt(rng, families):
+    """A prompt from one of a few families: a shared stem, then a random tail
+    (ids from a small vocabulary, so tails collide now and then)."""
+    stem = families[int(rng.integers(0, len(families)))]
+    cut = int(rng.integers(0, len(stem) + 1))
+    tail = rng.integers(0, 3, size=int(rng.integers(0, 40))).tolist()
+    return stem[:cut] + tail
+
+
+@pytest.mark.parametrize("size,total", [(4, 48), (16, 40), (1, 64)])
+def test_blocks_prefix_random_ops_match_oracle(size, total):
+    rng = np.random.default_rng(size * 1000 + total)
+    families = [rng.integers(0, 5, size=int(rng.integers(4, 90))).tolist() for _ in range(4)]
+    native, ref = feattn.Blocks(total, size, True), S.Blocks(total, size, True)
+    logs = {"native": [], "oracle": []}
+    gate = {"salt": 0}
+
+    def hooks(name):
+        def ready(key, page):
+            logs[name].append(("ready", key, page))
+            return (hash(key) + page + gate["salt"]) % 7 != 0
+        return ready, lambda key, page: logs[name].append(("evict", key, page))
+
+    r, e = hooks("native")
+    native.set_hooks(ready=r, evict=e)
+    ref.ready, ref.evict = hooks("oracle")
+    tokens = {}
+    for step in range(2500):
+        seq = int(rng.integers(0, 10))
+        if seq not in tokens:
+            tokens[seq] = _prompt(rng, families)
+        toks = tokens[seq]
+        op = rng.random()
+        if op < 0.2:
+            call = lambda b: b.probe(seq, toks)
+        elif op < 0.4:
+            target = int(rng.integers(0, len(toks) + 8))
+            call = lambda b: b.ensure(seq, target)
+        elif op < 0.6:
+            computed = int(rng.integers(0, len(toks) + 4))
+            call = lambda b: b.publish(seq, toks, computed)
+        elif op < 0.75:  # tokens committed (src/scheduler.cpp:94-99)
+            toks.extend(rng.integers(0, 3, size=int(rng.integers(1, 3 * size + 2))).tolist())
+            call = lambda b: None
+        elif op < 0.88:
+            call = lambda b: b.release(seq)
+        else:
+            call = lambda b: b.forget(seq)
+            tokens.pop(seq)
+        results = []
+        for b in (native, ref):
+            try:
+                results.append(call(b))
+            except (RuntimeError, ValueError):
+                results.append("error")
+        assert results[0] == results[1], (step, op, results)
+        if rng.random() < 0.05:
+            gate["salt"] += 1
+        assert native.table(seq) == ref.tables.get(seq, []), step
+        assert native.used() == ref.used() and native.free_pages() == ref.free_pages(), step
+        assert native.stats() == ref.stats(), step
+        assert logs["native"] == logs["oracle"], step
+        # what the mathematics fixes, independent of the oracle: every page is
+        # held by as many tables as list it, and a page two sequences share
+        # sits at the same index of both tables, whose tokens agree up to it
+        holders = {}
+        for other in tokens:
+            for i, page in enumerate(native.table(other)):
+                holders.setdefault(page, []).append((other, i))
+        assert native.used() == len(holders) and native.free_pages() == total - len(holders)
+        for page, where in holders.items():
+            if len(where) > 1:
+                i = where[0][1]
+                assert all(j == i for _, j in where), (page, where)
+                stems = {tuple(tokens[o][:(i + 1) * size]) for o, _ in where}
+                assert len(stems) == 1, (page, where)
+    native.close()
+
+
 def test_blocks_rejects_bad_pool():
     for total, size in ((0, 16), (2**31 - 1, 16), (4, 0), (-1, 16)):
         with pytest.raises(RuntimeError):

@@ -26,4 +26,5 @@ def test_planner_under_sanitizers(tmp_path):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="print_stacktrace=1")
     r = subprocess.run([str(exe), "1500", "600"], capture_output=True, text=True, timeout=300, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.startswith("ok: ")
+    lines = r.stdout.splitlines()
+    assert lines[-1].startswith("ok: ") and any(line.startswith("prefix cache: ") for line in lines)
