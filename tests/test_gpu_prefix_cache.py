@@ -9,8 +9,9 @@ in one batch.  A hit must be invisible: every output row and LSE is
 bit-identical to a run without the cache in which each sequence first
 recomputes the same prefix into pages of its own (the compared calls have the
 same shapes, so the same plan; only page ids differ), the K/V each sequence
-sees are bit-identical, and the cached run matches the oracle (tolerance:
-|a-b| <= 1e-2 + 1e-2*|b| on outputs, 1e-3 on the natural-log LSE)."""
+sees are bit-identical, and the cached run matches the oracle and, when oracle/_ref is
+built, the reference's own ATen attention (tolerance: |a-b| <= 1e-2 +
+1e-2*|b| on outputs, 1e-3 on the natural-log LSE)."""
 
 import math
 
@@ -21,6 +22,7 @@ import torch
 import feattn
 from feattn import workloads as W
 from oracle import aten_attention as A
+from oracle import ref_lib
 
 pytestmark = pytest.mark.gpu
 HQ, HKV, PAGE, DIM, VOCAB = 32, 8, 16, 128, 64
@@ -81,7 +83,7 @@ def serve(caching, cut, dtype, dev, oracle_checks=None):
         torch.cuda.synchronize()
         got[key] = (out.cpu(), lse.cpu())
         if oracle_checks is not None:
-            oracle_checks.append((key, b, q.cpu(), out.cpu(), lse.cpu()))
+            oracle_checks.append((key, b, q.clone(), out.cpu(), lse.cpu()))
         for s, e in zip(seqs, ends):
             blocks.publish(s, toks[s], e)
 
@@ -132,8 +134,13 @@ def test_prefix_cache_hits_are_invisible(dev, dtype):
         assert torch.equal(kv_of(blocks, s, n, vc), kv_of(pblocks, s, n, pvc)), s
     kcc, vcc = kc.cpu(), vc.cpu()
     for key, b, q, out, lse in checks:
-        want_out, want_lse = A.run(b, q, kcc, vcc, True)
+        want_out, want_lse = A.run(b, q.cpu(), kcc, vcc, True)
         torch.testing.assert_close(out.float(), want_out.float(), atol=1e-2, rtol=1e-2, msg=str(key))
         torch.testing.assert_close(lse, want_lse, atol=1e-3, rtol=0, msg=str(key))
+        if ref_lib.available():
+            # the reference's own create_plan / prepare_plan / attention
+            # (src/portable_gpu_ops.cpp:18-44) on the same device tensors
+            ref = ref_lib.attention(b, q, kc, vc, True).cpu()
+            torch.testing.assert_close(out.float(), ref.float(), atol=1e-2, rtol=1e-2, msg=str(key))
     blocks.close()
     pblocks.close()
