@@ -6,6 +6,8 @@ import os
 import re
 import subprocess
 
+import pytest
+
 import feattn
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -79,3 +81,25 @@ def test_error_reporting_without_device():
     rc = lib.fe_attn_plan_create(30, 8, 128, 16, 4, 4, 1, 16, ctypes.byref(h))
     assert rc == feattn.FE_EINVAL
 
+
+
+def test_headers_are_c99_and_resolve(tmp_path):
+    """The C headers compile as strict C99, and every function they declare
+    resolves against libfeattn.so from a C program (C linkage, exact names)."""
+    import shutil
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no C compiler")
+    names = sorted({n for h in HEADERS for n in header_functions(os.path.join(ROOT, "include", h))})
+    src = "".join(f'#include "{h}"\n' for h in HEADERS)
+    src += "typedef void (*fn)(void);\nstatic const fn table[] = {\n"
+    src += ",\n".join(f"  (fn)&{n}" for n in names)
+    src += "\n};\nint main(void) { return table[0] == 0; }\n"
+    c = tmp_path / "abi.c"
+    c.write_text(src)
+    lib_dir = os.path.dirname(feattn.LIB_PATH)
+    r = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror",
+                        "-I" + os.path.join(ROOT, "include"), str(c), "-o", str(tmp_path / "abi"),
+                        "-L" + lib_dir, "-lfeattn", "-Wl,-rpath-link,/opt/rocm/lib"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
