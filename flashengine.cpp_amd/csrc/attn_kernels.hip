@@ -66,7 +66,8 @@ constexpr int kDecUnit = 4096;  // 16 rows x 256 bytes: one K or V block, or one
 
 // Ring slots per wavefront.  Three (one unit in flight while a K/V pair is
 // computed) measured fastest: with 8 wavefronts per CU, deeper rings only
-// add queueing in the memory system.
+// add queueing in the memory system (with the non-temporal K/V reads too:
+// four slots took 99.5 against 98.7 us per headline step).
 #ifndef FEATTN_DECODE_UNITS
 #define FEATTN_DECODE_UNITS 3
 #endif
