@@ -18,7 +18,6 @@
 #include <cstring>
 #include <new>
 #include <string>
-#include <unordered_map>
 #include <vector>
 
 #include "attn_types.hpp"
@@ -307,18 +306,17 @@ void init_launch(Launch& L, const PlanShape& sh, bool bf16) {
 }
 
 // Launch sizes of the lists just staged.
-// Whether a tile list reads each K/V token once per kv head: no two of its
-// items cover different query columns of one (sequence, kv head).  Chunked
-// prefill cuts a long chunk into several column blocks that read the same
-// tokens, and those re-reads are L2 hits with the default policy (the
-// 8192-token prefill takes 0.257 ms so, 0.282 ms streamed); DFlash blocks
-// and short verify rows are one column block each.
-bool reads_tokens_once(const std::vector<WorkItem>& items) {
-  std::unordered_map<int64_t, int32_t> q0_of;
-  for (const WorkItem& w : items) {
-    const auto ins = q0_of.emplace(((int64_t)w.seq << 32) | (uint32_t)w.kvh, w.q0);
-    if (!ins.second && ins.first->second != w.q0) return false;
-  }
+// Whether the tile lists read each K/V token once per kv head: no sequence
+// with tile work is cut into several column blocks (the planner gives such a
+// sequence ceil(qlen / (kTileCols / group)) blocks, every one over the same
+// tokens).  Chunked prefill is cut so, and those re-reads are L2 hits with
+// the default policy (the 8192-token prefill takes 0.257 ms so, 0.282 ms
+// streamed); DFlash blocks and short verify rows are one block each.
+bool reads_tokens_once(const BuiltPlan& bp, const PlanShape& sh) {
+  const int group = sh.hq / sh.hkv;
+  const int rows_per_block = kTileCols / group;
+  for (const SeqInfo& s : bp.seqs)
+    if (s.qlen * group > kDecodeCols && s.qlen > rows_per_block) return false;
   return true;
 }
 
@@ -332,7 +330,7 @@ void record_lists(Launch& L, const BuiltPlan& bp, const HeapPlace& hp, int nc) {
     L.n_merge[m] = (int)bp.mode[m].merge.size();
     // Graph plans keep the policy their tile launch was captured with (a
     // cache hint: results do not depend on it).
-    const bool once = reads_tokens_once(bp.mode[m].tile);
+    const bool once = reads_tokens_once(bp, L.sh);
     if (L.graph && L.graph_stream[m] < 0) L.graph_stream[m] = once ? 1 : 0;
     L.tile_stream[m] = L.graph ? L.graph_stream[m] > 0 : once;
   }

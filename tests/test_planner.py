@@ -347,3 +347,40 @@ def test_random_batches_cover_and_lay_out_partials(seed):
     for causal in (True, False):
         coverage(b, causal)
         check_partial_slots(b, causal)
+
+
+def column_blocks_read_tokens_once(items):
+    """The tile items of one (sequence, kv head) all cover the same query
+    columns (their token ranges are then disjoint pieces)."""
+    q0_of = {}
+    for kind, seq, q0, nq, kvh, t0, t1, part in items:
+        if kind == 1 and q0_of.setdefault((seq, kvh), (q0, nq)) != (q0, nq):
+            return False
+    return True
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_single_column_block_rule(seed):
+    """The tile launch streams K/V with the non-temporal hint when no
+    sequence with tile work is cut into several column blocks; that is
+    decided from the query lengths alone (qlen <= 128 / group rows per
+    block), which must agree with the planner's actual lists."""
+    rng = np.random.default_rng(5000 + seed)
+    hq, hkv = HEAD_LAYOUTS[seed % len(HEAD_LAYOUTS)]
+    g = hq // hkv
+    batch = int(rng.integers(1, 7))
+    qlens = [int(rng.choice([1, 2, 16, 128 // g, 128 // g + 1, int(rng.integers(2, 200))])) for _ in range(batch)]
+    starts = [int(rng.integers(0, 3000)) for _ in range(batch)]
+    b = W.make_batch(hq, hkv, starts=starts, qlens=qlens, seed=seed)
+    rule = all(q * g <= 32 or q <= 128 // g for q in qlens)
+    for causal in (True, False):
+        assert column_blocks_read_tokens_once(feattn.dump(*plan_args(b), causal=causal)) == rule, (qlens, g)
+
+
+def test_single_column_block_rule_on_the_workloads():
+    """DFlash blocks stream; chunked prefill and the mixed step do not."""
+    want = {W.dflash_block: True, W.qwen3_8b_prefill: False, W.qwen3_30b_mixed: False}
+    for make, once in want.items():
+        b = make()
+        items = feattn.dump(*plan_args(b), causal=make is not W.dflash_block)
+        assert column_blocks_read_tokens_once(items) == once, make.__name__
