@@ -1,11 +1,12 @@
 // A C++ caller of libfeattn.so shaped like the reference's model runner
 // (src/cuda_model.cpp): graph buckets (common.cpp:45-51; the smallest bucket
 // that holds the batch gets a plan and a captured graph, :118, :150-157),
-// the FIFO page allocator
-// (scheduler.cpp:5,31,35), the per-step metadata (:131-142), and per layer
-// the q/k RMSNorm + RoPE + paged append followed by paged attention
-// (:91-96), all through the reference's fe::cuda:: signatures
-// (include/fe_native_hip.hpp).  A prefill step runs eagerly; decode steps
+// the FIFO page allocator with its prefix cache (scheduler.cpp:5-36), the
+// per-step metadata (:131-142), and per layer the q/k RMSNorm + RoPE + paged
+// append followed by paged attention (:91-96), all through the reference's
+// fe::cuda:: signatures (include/fe_native_hip.hpp).  Prefill steps run
+// eagerly: the prompts, then a request whose prompt starts with a published
+// prefix and computes only the rest over the shared pages; decode steps
 // replay a HIP graph captured once on the bucket's fixed buffers, with
 // prepare_plan called outside the capture as the reference does.
 //
@@ -184,26 +185,22 @@ int main(int argc, char** argv) {
     fe_check(fe_graph_buckets(kMaxSeqs, buckets.data(), nb, &nb), "fe_graph_buckets");
     out.vec("buckets", 2, buckets);
     fe_blocks* blocks = nullptr;
-    fe_check(fe_blocks_create(kPool, kPage, &blocks), "fe_blocks_create");
+    fe_check(fe_blocks_create_ex(kPool, kPage, 1, &blocks), "fe_blocks_create_ex");
 
     std::vector<Seq> seqs = {{1, 40}, {2, 5}, {3, 17}};
     const int n = (int)seqs.size();
 
-    // ---- step 0: chunked prefill of the prompts, eager, one plan sized for it
-    {
-      std::vector<int64_t> start(n, 0);
-      std::vector<int32_t> rows(n);
-      for (int i = 0; i < n; ++i) {
-        rows[i] = (int32_t)seqs[i].length;
-        int ok = 0;
-        fe_check(fe_blocks_ensure(blocks, seqs[i].id, seqs[i].length, &ok), "fe_blocks_ensure");
-        if (!ok) throw std::runtime_error("page pool exhausted");
-      }
-      Meta m = metadata(blocks, seqs, start, rows, n, 0);
+    // One prefill step run eagerly with a plan sized for it: metadata, then
+    // per layer the fused norm + RoPE + append and the attention; every
+    // input and output is recorded under `tag`.
+    auto eager_step = [&](const std::string& tag, const std::vector<Seq>& ss, const std::vector<int64_t>& start,
+                          const std::vector<int32_t>& rows) {
+      const int ns = (int)ss.size();
+      Meta m = metadata(blocks, ss, start, rows, ns, 0);
       const int R = (int)m.positions.size();
       fe::cuda::AttentionPlan* plan = fe::cuda::create_plan(kHq, kHkv, kDim, kPage, kMaxSeqs, kMaxLen / kPage + 1,
                                                             true, kPool);
-      fe::cuda::prepare_plan(plan, m.qo.data(), m.kv.data(), m.pages.data(), m.last.data(), n, R, false, st);
+      fe::cuda::prepare_plan(plan, m.qo.data(), m.kv.data(), m.pages.data(), m.last.data(), ns, R, false, st);
       int64_t* pos = dalloc<int64_t>(R);
       int64_t* slots = dalloc<int64_t>(R);
       hip_check(hipMemcpy(pos, m.positions.data(), R * 8, hipMemcpyHostToDevice), "hipMemcpy");
@@ -211,12 +208,12 @@ int main(int argc, char** argv) {
       uint16_t* qkv = dalloc<uint16_t>((size_t)R * kQkv);
       uint16_t* q = dalloc<uint16_t>((size_t)R * kHq * kDim);
       uint16_t* o = dalloc<uint16_t>((size_t)R * kHq * kDim);
-      out.vec("s0_qo", 1, m.qo);
-      out.vec("s0_kv", 1, m.kv);
-      out.vec("s0_pages", 1, m.pages);
-      out.vec("s0_last", 1, m.last);
-      out.vec("s0_positions", 2, m.positions);
-      out.vec("s0_slots", 2, m.slots);
+      out.vec(tag + "_qo", 1, m.qo);
+      out.vec(tag + "_kv", 1, m.kv);
+      out.vec(tag + "_pages", 1, m.pages);
+      out.vec(tag + "_last", 1, m.last);
+      out.vec(tag + "_positions", 2, m.positions);
+      out.vec(tag + "_slots", 2, m.slots);
       for (int l = 0; l < kLayers; ++l) {
         std::vector<uint16_t> x((size_t)R * kQkv);
         for (auto& v : x) v = rng.bf16();
@@ -225,7 +222,7 @@ int main(int argc, char** argv) {
                                   kDim, true, st, kMaxLen, (kPool + 1) * kPage);
         fe::cuda::attention(plan, q, kc[l], vc[l], o, true, st);
         hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
-        const std::string p = "s0_l" + std::to_string(l) + "_";
+        const std::string p = tag + "_l" + std::to_string(l) + "_";
         out.vec(p + "qkv", 0, x);
         out.device16(p + "q", {(uint64_t)R, kHq, kDim}, q);
         out.device16(p + "out", {(uint64_t)R, kHq, kDim}, o);
@@ -236,6 +233,68 @@ int main(int argc, char** argv) {
       (void)hipFree(qkv);
       (void)hipFree(q);
       (void)hipFree(o);
+    };
+    auto table_of = [&](int64_t id) {
+      int k = 0;
+      fe_check(fe_blocks_table(blocks, id, nullptr, 0, &k), "fe_blocks_table");
+      std::vector<int32_t> t(k);
+      fe_check(fe_blocks_table(blocks, id, t.data(), k, &k), "fe_blocks_table");
+      return t;
+    };
+
+    // token ids of the prompts (only the prefix cache reads them)
+    std::vector<std::vector<int64_t>> tokens(n);
+    for (int i = 0; i < n; ++i) {
+      for (int64_t t = 0; t < seqs[i].length; ++t) tokens[i].push_back((int64_t)(rng.next() % 1000));
+      out.vec("tokens" + std::to_string(seqs[i].id), 2, tokens[i]);
+    }
+
+    // ---- step 0: prefill of the prompts (nothing is published yet, so the
+    // probes find nothing), then their full pages are published
+    {
+      std::vector<int64_t> start(n, 0);
+      std::vector<int32_t> rows(n);
+      for (int i = 0; i < n; ++i) {
+        int64_t cached = -1;
+        fe_check(fe_blocks_probe(blocks, seqs[i].id, tokens[i].data(), seqs[i].length, &cached), "fe_blocks_probe");
+        if (cached != 0) throw std::runtime_error("empty prefix cache reported a hit");
+        rows[i] = (int32_t)seqs[i].length;
+        int ok = 0;
+        fe_check(fe_blocks_ensure(blocks, seqs[i].id, seqs[i].length, &ok), "fe_blocks_ensure");
+        if (!ok) throw std::runtime_error("page pool exhausted");
+      }
+      eager_step("s0", seqs, start, rows);
+      for (int i = 0; i < n; ++i)
+        fe_check(fe_blocks_publish(blocks, seqs[i].id, tokens[i].data(), seqs[i].length, seqs[i].length),
+                 "fe_blocks_publish");
+    }
+
+    // ---- a request whose first 36 tokens are sequence 1's: the probe hands
+    // it sequence 1's two full pages (32 tokens), and it computes its last 8
+    // rows into a page of its own over them; it finishes after this step
+    {
+      Seq late{4, 40};
+      std::vector<int64_t> t4(tokens[0].begin(), tokens[0].begin() + 36);
+      for (int k = 0; k < 4; ++k) t4.push_back((int64_t)(rng.next() % 1000));
+      out.vec("tokens4", 2, t4);
+      int64_t cached = -1;
+      fe_check(fe_blocks_probe(blocks, late.id, t4.data(), late.length, &cached), "fe_blocks_probe");
+      int ok = 0;
+      fe_check(fe_blocks_ensure(blocks, late.id, late.length, &ok), "fe_blocks_ensure");
+      if (!ok) throw std::runtime_error("page pool exhausted");
+      const std::vector<int32_t> t = table_of(late.id), t1 = table_of(seqs[0].id);
+      if (cached != 32 || t.size() != 3 || t[0] != t1[0] || t[1] != t1[1] || t[2] == t1[2])
+        throw std::runtime_error("prefix cache did not share sequence 1's pages");
+      out.vec("p_cached", 2, std::vector<int64_t>{cached});
+      eager_step("p", {late}, {cached}, {(int32_t)(late.length - cached)});
+      fe_check(fe_blocks_forget(blocks, late.id), "fe_blocks_forget");
+      fe_prefix_stats ps{};
+      fe_check(fe_blocks_prefix_stats(blocks, &ps), "fe_blocks_prefix_stats");
+      out.vec("prefix_stats", 2,
+              std::vector<int64_t>{ps.requests, ps.hit_requests, ps.cached_blocks, ps.new_blocks, ps.resident_blocks,
+                                   ps.evictions});
+      std::printf("prefix step done (cached %lld)\n", (long long)cached);
+      std::fflush(stdout);
     }
 
     // ---- decode steps through the graph of the smallest bucket >= n

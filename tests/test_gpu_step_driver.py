@@ -1,10 +1,12 @@
 """The C++ caller in tests/cpp/step_driver.cpp drives libfeattn.so through
 the reference's fe::cuda:: signatures the way src/cuda_model.cpp does (page
-allocator, per-step metadata, q/k RMSNorm + RoPE + paged append and paged
-attention per layer, an eager prefill step, then decode steps replayed from a
+allocator with its prefix cache, per-step metadata, q/k RMSNorm + RoPE +
+paged append and paged attention per layer, an eager prefill step, a request
+that reuses a published prefix's pages, then decode steps replayed from a
 captured HIP graph with a padded bucket).  It writes every input and output;
-this test replays the same sequence on the oracle: metadata and caches
-bit-exact, attention outputs within 1e-2 abs / 1e-2 rel."""
+this test replays the same sequence on the oracle: allocator decisions,
+metadata and caches bit-exact, attention outputs within 1e-2 abs / 1e-2
+rel."""
 
 import os
 import struct
@@ -76,8 +78,9 @@ def test_cpp_step_driver_vs_oracle(dev, tmp_path):
     r = read_records(path)
     assert r["buckets"].tolist() == S.graph_buckets(4) == [1, 2, 4]
     table = r["rope_table"]
-    blocks = S.Blocks(POOL, PAGE)
+    blocks = S.Blocks(POOL, PAGE, caching=True)
     ids, lens = [1, 2, 3], [40, 5, 17]
+    tokens = {i: r[f"tokens{i}"].tolist() for i in ids}
     kc = [np.zeros((CSLOTS, HKV * D), np.uint16) for _ in range(LAYERS)]
     vc = [np.zeros((CSLOTS, HKV * D), np.uint16) for _ in range(LAYERS)]
 
@@ -90,14 +93,34 @@ def test_cpp_step_driver_vs_oracle(dev, tmp_path):
         want = attention_oracle(m, starts, qlens, tables, bf(q, (rows, HQ, D)), kc[l], vc[l])
         torch.testing.assert_close(bf(got_out, (rows, HQ, D)).float(), want.float(), atol=1e-2, rtol=1e-2)
 
-    # step 0: eager prefill of the prompts
+    # step 0: eager prefill of the prompts, then their full pages published
     for i, n in zip(ids, lens):
+        assert blocks.probe(i, tokens[i]) == 0
         assert blocks.ensure(i, n)
     tables = [blocks.tables[i] for i in ids]
     m = check_step(r, "s0", [0, 0, 0], lens, tables, 3, 0)
     rows = sum(lens)
     for l in range(LAYERS):
         layer(l, r[f"s0_l{l}_qkv"], m, rows, [0, 0, 0], lens, tables, r[f"s0_l{l}_out"], r[f"s0_l{l}_q"])
+    for i, n in zip(ids, lens):
+        blocks.publish(i, tokens[i], n)
+    # a request sharing sequence 1's first 36 tokens: two shared pages, its
+    # last 8 rows computed over them (src/scheduler.cpp:6-17)
+    t4 = r["tokens4"].tolist()
+    assert t4[:36] == tokens[1][:36] and len(t4) == 40
+    cached = blocks.probe(4, t4)
+    assert cached == 32 == r["p_cached"][0]
+    assert blocks.ensure(4, 40)
+    t4_table = blocks.tables[4]
+    assert t4_table[:2] == blocks.tables[1][:2] and t4_table[2] not in blocks.tables[1]
+    m = check_step(r, "p", [32], [8], [t4_table], 1, 0)
+    for l in range(LAYERS):
+        layer(l, r[f"p_l{l}_qkv"], m, 8, [32], [8], [t4_table], r[f"p_l{l}_out"], r[f"p_l{l}_q"])
+    blocks.forget(4)
+    st = blocks.stats()
+    assert r["prefix_stats"].tolist() == [st[k] for k in (
+        "prefix_requests", "prefix_hit_requests", "prefix_cached_blocks", "prefix_new_blocks",
+        "prefix_resident_blocks", "prefix_evictions")] == [4, 1, 2, 3, 3, 0]
     # decode steps 1-3 through the graph of bucket 4 (one padding entry)
     for step in (1, 2, 3):
         starts = list(lens)
